@@ -1,0 +1,227 @@
+/*
+ * sca_hip.h - C ABI of the MI355X (gfx950) kernel library `libsca_hip.so`.
+ *
+ * This is the only header through which host code reaches the GPU. Every HIP runtime call and
+ * every kernel launch of the attention stack lives behind these functions; the C++ host layer
+ * (sca:: API, dispatcher, KV cache) and any foreign-language binding (ctypes, cgo, JNI) call them
+ * with plain pointers, sizes and POD structs. No C++ or framework types cross this boundary.
+ *
+ * Conventions
+ *   - Every function returning `int` returns 0 on success. A positive value below 2000 is a
+ *     hipError_t; 2001..2010 are the attention status codes (SCA_E_*); the text of the last
+ *     failure on the calling thread is available from sca_hip_last_error_string().
+ *   - Pointers named q/k/v/out/lse/partial_* / page_table / seq_lens / slot_mapping /
+ *     block_ids are device pointers and are borrowed for the duration of the (asynchronous)
+ *     launch. Scratch (split-K partials) is always caller-provided: the library allocates no
+ *     device memory on any launch path.
+ *   - `stream` is a hipStream_t passed as void*; NULL means the default stream.
+ *   - Thread-compatible: concurrent calls on different streams are safe; the library keeps no
+ *     mutable device state.
+ *
+ * Each launch entry point replaces one device-side entry point of the reference
+ * (DeRuiChen258/SciCompute-Attention); the replaced declaration is cited above each function.
+ */
+#ifndef SCA_HIP_H_
+#define SCA_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define SCA_HIP_API __attribute__((visibility("default")))
+#else
+#define SCA_HIP_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------------------------- */
+/* status codes                                                                                 */
+/* ------------------------------------------------------------------------------------------- */
+enum {
+    SCA_OK = 0,
+    SCA_E_UNSUPPORTED_HEAD_DIM = 2001,
+    SCA_E_UNSUPPORTED_DTYPE = 2002,
+    SCA_E_UNSUPPORTED_LAYOUT = 2003,
+    SCA_E_LAYOUT_MISMATCH = 2004,
+    SCA_E_SHAPE_MISMATCH = 2005,
+    SCA_E_SEQ_TOO_LONG = 2006,
+    SCA_E_KV_CAPACITY = 2007,
+    SCA_E_WORKSPACE = 2008,
+    SCA_E_UNSUPPORTED_FEATURE = 2009,
+    SCA_E_DEVICE_CAPABILITY = 2010
+};
+
+/* Element type of Q/K/V/O (the compute dtype ids of the reference's launchers). */
+enum { SCA_DTYPE_F32 = 0, SCA_DTYPE_F16 = 1, SCA_DTYPE_BF16 = 2 };
+
+/* Message of the last failing call on this thread ("" when none). Never NULL. */
+SCA_HIP_API const char* sca_hip_last_error_string(void);
+
+/* ------------------------------------------------------------------------------------------- */
+/* device probe                                                                                 */
+/* replaces: src/runtime/device_probe.h:14-36 (ScaDeviceProbe, sca_probe_device,                */
+/*           sca_mem_get_info)                                                                  */
+/* ------------------------------------------------------------------------------------------- */
+#define SCA_HIP_DEVICE_NAME_MAX 256
+
+typedef struct ScaHipDeviceProbe {
+    char name[SCA_HIP_DEVICE_NAME_MAX];
+    char arch_name[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int major;
+    int minor;
+    int cu_count;                /* multiProcessorCount (compute units) */
+    int wave_size;               /* 64 on CDNA */
+    int clock_khz;               /* peak shader clock */
+    int memory_clock_khz;
+    int memory_bus_width_bits;
+    unsigned long long lds_per_cu;             /* maxSharedMemoryPerMultiProcessor */
+    unsigned long long lds_per_block;          /* sharedMemPerBlock */
+    unsigned long long regs_per_cu;
+    unsigned long long max_threads_per_cu;
+    unsigned long long l2_bytes;
+    unsigned long long total_mem_bytes;
+    unsigned long long free_mem_bytes;
+    int gpu_available;           /* 1 when a HIP device was found */
+    int binary_has_gfx950;       /* this library carries gfx950 code objects (MFMA f16/bf16 K=16) */
+} ScaHipDeviceProbe;
+
+SCA_HIP_API int sca_hip_probe_device(int device_id, ScaHipDeviceProbe* out);
+SCA_HIP_API int sca_hip_mem_get_info(unsigned long long* free_bytes,
+                                     unsigned long long* total_bytes);
+SCA_HIP_API int sca_hip_get_device_count(int* count);
+
+/* ------------------------------------------------------------------------------------------- */
+/* memory, streams, events (the plumbing the host layer's sci::Device/Stream use)               */
+/* ------------------------------------------------------------------------------------------- */
+enum { SCA_COPY_H2D = 1, SCA_COPY_D2H = 2, SCA_COPY_D2D = 3, SCA_COPY_H2H = 4 };
+
+SCA_HIP_API int sca_hip_malloc(void** ptr, size_t bytes);
+SCA_HIP_API int sca_hip_free(void* ptr);
+SCA_HIP_API int sca_hip_host_malloc(void** ptr, size_t bytes); /* pinned host memory */
+SCA_HIP_API int sca_hip_host_free(void* ptr);
+SCA_HIP_API int sca_hip_memcpy(void* dst, const void* src, size_t bytes, int kind);
+SCA_HIP_API int sca_hip_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
+                                     void* stream);
+/* Zero-fill with a kernel (graph-capture safe, unlike a memset node). */
+SCA_HIP_API int sca_hip_zero_async(void* ptr, size_t bytes, void* stream);
+SCA_HIP_API int sca_hip_device_synchronize(void);
+SCA_HIP_API int sca_hip_stream_create(void** stream);
+SCA_HIP_API int sca_hip_stream_destroy(void* stream);
+SCA_HIP_API int sca_hip_stream_synchronize(void* stream);
+SCA_HIP_API int sca_hip_event_create(void** event);
+SCA_HIP_API int sca_hip_event_destroy(void* event);
+SCA_HIP_API int sca_hip_event_record(void* event, void* stream);
+SCA_HIP_API int sca_hip_event_synchronize(void* event);
+SCA_HIP_API int sca_hip_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ------------------------------------------------------------------------------------------- */
+/* flash prefill                                                                                */
+/* replaces: src/backends/flash/flash_fwd_kernel.cuh:32-60 (FlashFwdParams, FlashSmemBytesFor,  */
+/*           LaunchFlashFwd)                                                                    */
+/* ------------------------------------------------------------------------------------------- */
+typedef struct sca_flash_params {
+    const void* q;       /* element (b,h,s,d) at b*q_sb + h*q_sh + s*q_ss + d */
+    const void* k;
+    const void* v;
+    void* out;
+    float* lse;          /* optional FP32 [b,h,s] at (b*num_heads + h)*seq_q + s; NULL = none */
+    int64_t batch;
+    int64_t num_heads;   /* H_q */
+    int64_t num_kv_heads;/* H_kv; H_q % H_kv == 0, kv head = h / (H_q/H_kv) */
+    int64_t seq_q;
+    int64_t seq_kv;
+    int64_t head_dim;    /* 32, 64, 96, 128, 160, 192 or 256 */
+    int64_t q_sb, q_sh, q_ss;
+    int64_t k_sb, k_sh, k_ss;
+    int64_t v_sb, v_sh, v_ss;
+    int64_t o_sb, o_sh, o_ss;
+    float scale;         /* softmax scale (already resolved, > 0) */
+    int32_t causal;      /* bottom-right aligned: key j visible from row i iff j <= i + diagonal */
+    int32_t dtype;       /* SCA_DTYPE_F16 or SCA_DTYPE_BF16 */
+    int64_t diagonal;    /* seq_kv - seq_q when causal */
+} sca_flash_params;
+
+/* LDS bytes one workgroup of the flash kernel uses for this head_dim (-1 if not built). */
+SCA_HIP_API int64_t sca_hip_flash_lds_bytes(int32_t head_dim, int64_t elem_bytes);
+/* Tile geometry of the flash kernel for head_dim: rows per workgroup, keys per tile, waves. */
+SCA_HIP_API int sca_hip_flash_tile(int32_t head_dim, int32_t* block_m, int32_t* block_n,
+                                   int32_t* waves, int32_t* stages);
+SCA_HIP_API int sca_hip_flash_fwd(const sca_flash_params* params, void* stream);
+
+/* ------------------------------------------------------------------------------------------- */
+/* split-K decode (contiguous and paged)                                                        */
+/* replaces: src/backends/decode/decode_splitk.cuh:15-57 (DecodeFwdParams, LaunchDecodeSplitK,  */
+/*           LaunchDecodeSplitKPaged) and src/backends/paged/paged_attention.cuh:21-32          */
+/*           (LaunchPagedAttention)                                                             */
+/* ------------------------------------------------------------------------------------------- */
+typedef struct sca_decode_params {
+    const void* q;        /* one query token per (b, h): element at b*q_sb + h*q_sh + d */
+    const void* k;        /* contiguous: b*k_sb + h_kv*k_sh + j*k_ss + d;                  */
+    const void* v;        /* paged: layer base, row r at r*k_ss + h_kv*k_sh + d            */
+    void* out;            /* element at b*o_sb + h*o_sh + d */
+    float* partial_m;     /* [batch*num_heads*num_splits], flat ((b*H_q)+h)*splits + s */
+    float* partial_l;     /* same indexing */
+    float* partial_o;     /* [batch*num_heads*num_splits, head_dim] */
+    int64_t batch;
+    int64_t num_heads;
+    int64_t num_kv_heads;
+    int64_t seq_kv;       /* contiguous length, or the upper bound when seq_lens is NULL */
+    int64_t head_dim;     /* multiple of 32, <= 256 */
+    int64_t num_splits;   /* >= 1 */
+    int64_t q_sb, q_sh;
+    int64_t k_sb, k_sh, k_ss;
+    int64_t v_sb, v_sh, v_ss;
+    int64_t o_sb, o_sh;
+    float scale;
+    int32_t dtype;        /* SCA_DTYPE_F32, F16 or BF16 */
+    /* paged addressing (page_table != NULL): row = page_table[b*max_blocks_per_seq + j/bs]*bs
+     * + j%bs; entries < 0 or >= num_kv_blocks contribute nothing */
+    const int32_t* page_table;
+    int64_t block_size;
+    int64_t max_blocks_per_seq;
+    int64_t num_kv_blocks;
+    const int32_t* seq_lens; /* optional per-sequence lengths (device), else seq_kv for all */
+} sca_decode_params;
+
+/* FP32 scratch elements the partials need: batch*num_heads*num_splits*(2 + head_dim). */
+SCA_HIP_API int64_t sca_hip_decode_partial_elements(int64_t batch, int64_t num_heads,
+                                                    int64_t num_splits, int64_t head_dim);
+SCA_HIP_API int sca_hip_decode_splitk(const sca_decode_params* params, void* stream);
+SCA_HIP_API int sca_hip_decode_splitk_paged(const sca_decode_params* params, void* stream);
+
+/* ------------------------------------------------------------------------------------------- */
+/* KV cache data movement over the block-major layout [num_blocks][block_size][H_kv][D]         */
+/* replaces: src/kv_cache/kv_cache_kernels.cuh:20-33 (LaunchKvAppend, LaunchKvResetBlock,       */
+/*           LaunchKvGather)                                                                    */
+/* ------------------------------------------------------------------------------------------- */
+typedef struct sca_kv_shape {
+    int64_t num_blocks;
+    int64_t block_size;
+    int64_t num_kv_heads;
+    int64_t head_dim;
+} sca_kv_shape;
+
+/* dst row `slot` of K and V <- row t of k_new/v_new ([num_tokens, H_kv, D]); slot < 0 or a block
+ * beyond num_blocks skips the token. */
+SCA_HIP_API int sca_hip_kv_append(void* layer_k, void* layer_v, const void* k_new,
+                                  const void* v_new, const int32_t* slot_mapping,
+                                  int64_t num_tokens, const sca_kv_shape* shape,
+                                  int64_t elem_bytes, void* stream);
+/* Zeroes K and V of the listed blocks (ids outside [0, num_blocks) are skipped). */
+SCA_HIP_API int sca_hip_kv_reset_blocks(void* layer_k, void* layer_v, const int32_t* block_ids,
+                                        int64_t num_block_ids, const sca_kv_shape* shape,
+                                        int64_t elem_bytes, void* stream);
+/* out[i] <- block block_ids[i] of `layer` (out is [n, block_size, H_kv, D]); invalid ids give
+ * zero rows. */
+SCA_HIP_API int sca_hip_kv_gather(const void* layer, const int32_t* block_ids,
+                                  int64_t num_block_ids, void* out, const sca_kv_shape* shape,
+                                  int64_t elem_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SCA_HIP_H_ */

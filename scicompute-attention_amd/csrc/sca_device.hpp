@@ -1,0 +1,81 @@
+// Device-side helpers shared by the gfx950 kernels: vector types for the MFMA operands, dtype
+// conversion, cross-lane helpers and the thread-local error text of the C ABI.
+//
+// Written for CDNA4 (wave64, MFMA f32_32x32x16_{f16,bf16}); there is no other target.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "sca_hip.h"
+
+namespace sca_hip {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Storage types. Element bits are moved as uint16_t and reinterpreted at the MFMA boundary so
+// that the load/store code is shared by fp16 and bf16.
+struct F16 {
+    using vec8 = half8;
+    static __device__ __forceinline__ float to_float(uint16_t bits) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+    }
+    // IEEE round-to-nearest-even (v_cvt_f16_f32).
+    static __device__ __forceinline__ uint16_t from_float(float x) {
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+    }
+};
+
+struct BF16 {
+    using vec8 = bf16x8;
+    static __device__ __forceinline__ float to_float(uint16_t bits) {
+        return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16);
+    }
+    // Round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
+    static __device__ __forceinline__ uint16_t from_float(float x) {
+        return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+    }
+};
+
+struct F32 {
+    static __device__ __forceinline__ float to_float(float x) { return x; }
+    static __device__ __forceinline__ float from_float(float x) { return x; }
+};
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+
+// v_exp_f32: 2^x. exp2(-inf) = 0, which keeps masked logits exactly out of every sum.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Swap halves of the wave: lane l receives the value of lane l ^ 32.
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
+
+// 16-lane butterfly sums (DPP-friendly offsets 8,4,2,1 stay inside one 16-lane row).
+__device__ __forceinline__ float row16_sum(float x) {
+    x += __shfl_xor(x, 8);
+    x += __shfl_xor(x, 4);
+    x += __shfl_xor(x, 2);
+    x += __shfl_xor(x, 1);
+    return x;
+}
+
+}  // namespace sca_hip
+
+// Error reporting of the C ABI (defined in runtime.hip).
+namespace sca_hip {
+int SetError(int code, const std::string& message);
+int CheckLaunch(const char* what, hipStream_t stream);
+}  // namespace sca_hip

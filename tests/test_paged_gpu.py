@@ -1,0 +1,133 @@
+"""Paged decode parity on the GPU through sca_hip_decode_splitk_paged, against the FP64 oracle
+applied to the page-table gather of the block-major pool (page_table.cuh:18-36).
+
+Case lists follow tests/kernel/test_paged_correctness.cu:134-166, with a seeded random
+permutation as the block table (the reference's own tests only ever see ascending LIFO ids).
+"""
+
+import numpy as np
+import pytest
+
+import oracle.oracle as orc
+import sca_amd
+from sca_amd import hip as H
+from attn_util import check_attention, decode_params, normal, quantize, uniform, to_float, \
+    ELEM_BYTES
+
+pytestmark = pytest.mark.gpu
+
+
+def build_pool(lengths, bs, Hkv, D, dtype, seed, slack=3, gen="uniform"):
+    """Block-major pool [num_blocks, bs, Hkv, D] with a permuted block table per sequence."""
+    rng = np.random.default_rng(seed)
+    need = [(L + bs - 1) // bs for L in lengths]
+    num_blocks = sum(need) + slack
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    max_blocks = max(max(need), 1) + 2
+    table = np.full((len(lengths), max_blocks), -1, np.int32)
+    pos = 0
+    for s, n in enumerate(need):
+        table[s, :n] = perm[pos:pos + n]
+        pos += n
+    shape = (num_blocks, bs, Hkv, D)
+    if gen == "uniform":
+        k, v = uniform(shape, seed + 11), uniform(shape, seed + 22)
+    else:
+        k, v = normal(shape, seed + 11), normal(shape, seed + 22)
+    kb, kd = quantize(k, dtype)
+    vb, vd = quantize(v, dtype)
+    return num_blocks, max_blocks, table, kb, kd, vb, vd
+
+
+def run_paged(qb, kb, vb, table, lengths, dtype, *, Hq, Hkv, D, bs, num_blocks, splits,
+              pass_lens=True):
+    S = len(lengths)
+    max_blocks = table.shape[1]
+    dq = H.DeviceBuffer.from_array(qb)
+    dk = H.DeviceBuffer.from_array(kb)
+    dv = H.DeviceBuffer.from_array(vb)
+    dt = H.DeviceBuffer.from_array(table)
+    dl = H.DeviceBuffer.from_array(np.asarray(lengths, np.int32))
+    dout = H.DeviceBuffer(S * Hq * D * ELEM_BYTES[dtype])
+    parts = H.DeviceBuffer(4 * sca_amd.hip_lib().sca_hip_decode_partial_elements(S, Hq, splits, D))
+    p = decode_params(dq, dk, dv, dout, parts, B=S, Hq=Hq, Hkv=Hkv, Skv=num_blocks * bs, D=D,
+                      splits=splits, dtype=dtype, k_strides=(0, D, Hkv * D))
+    p.page_table = dt.ptr
+    p.block_size = bs
+    p.max_blocks_per_seq = max_blocks
+    p.num_kv_blocks = num_blocks
+    p.seq_lens = dl.ptr if pass_lens else None
+    H.decode_splitk_paged(p)
+    sca_amd.synchronize()
+    return to_float(dout.download(np.uint16), dtype).reshape(S, Hq, D)
+
+
+def reference(qd, kd, vd, table, lengths, bs, num_blocks):
+    outs = []
+    for s, L in enumerate(lengths):
+        kc, valid = orc.paged_gather(kd, table[s], L, bs, num_blocks)
+        vc, _ = orc.paged_gather(vd, table[s], L, bs, num_blocks)
+        kc, vc = kc[:, valid], vc[:, valid]
+        o, _ = orc.reference_attention(qd[s:s + 1], kc[None], vc[None], True)
+        outs.append(o)
+    return np.concatenate(outs)
+
+
+def _case(lengths, bs, Hq, Hkv, D, dtype, seed, splits=16, gen="uniform"):
+    nb, mb, table, kb, kd, vb, vd = build_pool(lengths, bs, Hkv, D, dtype, seed, gen=gen)
+    q = uniform((len(lengths), Hq, 1, D), seed) if gen == "uniform" else \
+        normal((len(lengths), Hq, 1, D), seed)
+    qb, qd = quantize(q, dtype)
+    out = run_paged(qb, kb, vb, table, lengths, dtype, Hq=Hq, Hkv=Hkv, D=D, bs=bs, num_blocks=nb,
+                    splits=splits)
+    ref = reference(qd, kd, vd, table, lengths, bs, nb)
+    tag = f"paged {dtype} lens={lengths[:4]} bs={bs} Hq={Hq} Hkv={Hkv} D={D} splits={splits}"
+    print(tag, flush=True)
+    check_attention(out.reshape(-1, D), ref, dtype, tag)
+
+
+@pytest.mark.parametrize("bs", [1, 8, 16, 32])
+def test_every_block_size(hip, bs):
+    _case([257], bs, 8, 8, 128, "f16", 80000 + bs)
+
+
+@pytest.mark.parametrize("group", [1, 2, 4])
+def test_gqa_and_lengths(hip, group):
+    for j, L in enumerate([33, 129, 512]):
+        _case([L], 16, 8 * group, 8, 64, "f16", 81000 + 3 * group + j)
+
+
+def test_many_ragged_sequences_bf16(hip):
+    rng = np.random.default_rng(5)
+    lengths = rng.integers(1, 3000, size=12).tolist()
+    _case(lengths, 16, 32, 8, 128, "bf16", 82001, gen="normal")
+    _case(lengths, 16, 32, 8, 128, "bf16", 82002, splits=1, gen="normal")
+
+
+def test_unmapped_pages_contribute_nothing(hip):
+    # a -1 hole and an out-of-pool id in the middle of the table: those tokens are skipped
+    lengths = [160]
+    bs, Hq, Hkv, D = 16, 8, 2, 128
+    nb, mb, table, kb, kd, vb, vd = build_pool(lengths, bs, Hkv, D, "f16", 83001)
+    table[0, 3] = -1
+    table[0, 5] = nb + 7
+    q = uniform((1, Hq, 1, D), 83001)
+    qb, qd = quantize(q, "f16")
+    out = run_paged(qb, kb, vb, table, lengths, "f16", Hq=Hq, Hkv=Hkv, D=D, bs=bs, num_blocks=nb,
+                    splits=4)
+    ref = reference(qd, kd, vd, table, lengths, bs, nb)
+    check_attention(out.reshape(-1, D), ref, "f16", "paged holes")
+
+
+def test_null_seq_lens_uses_pool_upper_bound(hip):
+    # without seq_lens every mapped page of the row is attended in full (decode_splitk.cu:102)
+    lengths = [40]
+    bs, Hq, Hkv, D = 16, 4, 4, 64
+    nb, mb, table, kb, kd, vb, vd = build_pool(lengths, bs, Hkv, D, "f16", 84001)
+    q = uniform((1, Hq, 1, D), 84001)
+    qb, qd = quantize(q, "f16")
+    out = run_paged(qb, kb, vb, table, lengths, "f16", Hq=Hq, Hkv=Hkv, D=D, bs=bs, num_blocks=nb,
+                    splits=4, pass_lens=False)
+    full = 3 * bs  # 3 mapped pages
+    ref = reference(qd, kd, vd, table, [full], bs, nb)
+    check_attention(out.reshape(-1, D), ref, "f16", "paged null seq_lens")
