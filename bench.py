@@ -1,0 +1,307 @@
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Workloads (inputs synthetic, seeded, resident in HBM before timing):
+  * C2  flash prefill fp16, B=1, H=8, D=128, S=4096, causal (the headline `value`) and
+        non-causal;
+  * C5  paged decode bf16, 64 sequences with lengths U[512,16384], block size 16, block-major pool
+        with a seeded permuted block table, H_q=32, H_kv=8, D=128; each step appends one token per
+        sequence (host block bookkeeping + the append kernel), then attends; the attend kernel is
+        timed;
+  * C4  split-K decode fp16, B=16, H_q=32, H_kv=8, D=128, S_kv=4096.
+A step of C2 is one flash launch over the whole batch. Kernel time is measured with HIP events
+recorded on the launch stream around the K timed launches; the algorithmic work per launch
+(FLOPs or bytes) divided by the average launch time gives the achieved rate.
+
+The CPU baseline is the naive three-pass FP32 restatement of the reference's naive backend
+(oracle/sca_oracle.c, attention_naive.cu:41-135) timed on a bounded sample of C2 (one head)
+on the host cores.
+
+Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(REPO, "scicompute-attention_amd", "python"), REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import sca_amd  # noqa: E402
+from sca_amd import hip as H  # noqa: E402
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
+
+
+def causal_flops(B, H_, S, D):
+    return 4 * B * H_ * D * (S * (S + 1) // 2)
+
+
+def f16_bits(rng, shape):
+    return rng.standard_normal(size=shape, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def bf16_bits(rng, shape, chunk=1 << 24):
+    """Seeded N(0,1) bf16 bits; large tensors tile one random chunk (the values do not change
+    the amount of work)."""
+    n = int(np.prod(shape))
+    m = min(n, chunk)
+    x = rng.standard_normal(size=m, dtype=np.float32).view(np.uint32)
+    bits = ((x + 0x7FFF + ((x >> 16) & 1)) >> 16).astype(np.uint16)
+    if m < n:
+        bits = np.resize(bits, n)
+    return bits.reshape(shape)
+
+
+def time_launches(launch, steps, warmup):
+    for _ in range(warmup):
+        launch()
+    sca_amd.synchronize()
+    start, stop = H.Event(), H.Event()
+    start.record()
+    for _ in range(steps):
+        launch()
+    stop.record()
+    stop.synchronize()
+    sca_amd.synchronize()
+    return start.elapsed_ms(stop) / steps
+
+
+# ---- C2: flash prefill -------------------------------------------------------------------------
+def bench_flash(steps, warmup, causal, B=1, Hh=8, S=4096, D=128):
+    rng = np.random.default_rng(2024)
+    dq = H.DeviceBuffer.from_array(f16_bits(rng, (B, Hh, S, D)))
+    dk = H.DeviceBuffer.from_array(f16_bits(rng, (B, Hh, S, D)))
+    dv = H.DeviceBuffer.from_array(f16_bits(rng, (B, Hh, S, D)))
+    dout = H.DeviceBuffer(B * Hh * S * D * 2)
+    p = H.FlashParams()
+    p.q, p.k, p.v, p.out, p.lse = dq.ptr, dk.ptr, dv.ptr, dout.ptr, None
+    p.batch, p.num_heads, p.num_kv_heads, p.seq_q, p.seq_kv, p.head_dim = B, Hh, Hh, S, S, D
+    p.q_sb, p.q_sh, p.q_ss = Hh * S * D, S * D, D
+    p.k_sb, p.k_sh, p.k_ss = p.q_sb, p.q_sh, p.q_ss
+    p.v_sb, p.v_sh, p.v_ss = p.q_sb, p.q_sh, p.q_ss
+    p.o_sb, p.o_sh, p.o_ss = p.q_sb, p.q_sh, p.q_ss
+    p.scale = float(np.float32(1.0 / np.sqrt(D)))
+    p.causal = 1 if causal else 0
+    p.dtype = H.DTYPE_F16
+    p.diagonal = 0
+    ms = time_launches(lambda: H.flash_fwd(p), steps, warmup)
+    flops = causal_flops(B, Hh, S, D) if causal else 4 * B * Hh * S * S * D
+    return {"ms": ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
+            "bytes": 4 * B * Hh * S * D * 2}
+
+
+# ---- C4: split-K decode --------------------------------------------------------------------------
+def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=8):
+    rng = np.random.default_rng(4004)
+    dq = H.DeviceBuffer.from_array(f16_bits(rng, (B, Hq, 1, D)))
+    dk = H.DeviceBuffer.from_array(f16_bits(rng, (B, Hkv, S, D)))
+    dv = H.DeviceBuffer.from_array(f16_bits(rng, (B, Hkv, S, D)))
+    dout = H.DeviceBuffer(B * Hq * D * 2)
+    parts = H.DeviceBuffer(4 * sca_amd.hip_lib().sca_hip_decode_partial_elements(B, Hq, splits, D))
+    p = H.DecodeParams()
+    p.q, p.k, p.v, p.out = dq.ptr, dk.ptr, dv.ptr, dout.ptr
+    base = B * Hq * splits
+    p.partial_m, p.partial_l, p.partial_o = parts.ptr, parts.ptr + 4 * base, parts.ptr + 8 * base
+    p.batch, p.num_heads, p.num_kv_heads, p.seq_kv, p.head_dim, p.num_splits = B, Hq, Hkv, S, D, splits
+    p.q_sb, p.q_sh = Hq * D, D
+    p.k_sb, p.k_sh, p.k_ss = Hkv * S * D, S * D, D
+    p.v_sb, p.v_sh, p.v_ss = p.k_sb, p.k_sh, p.k_ss
+    p.o_sb, p.o_sh = Hq * D, D
+    p.scale = float(np.float32(1.0 / np.sqrt(D)))
+    p.dtype = H.DTYPE_F16
+    ms = time_launches(lambda: H.decode_splitk(p), steps, warmup)
+    nbytes = 2 * B * Hkv * S * D * 2 + 2 * B * Hq * D * 2
+    return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9, "splits": splits}
+
+
+# ---- C5: paged decode ------------------------------------------------------------------------------
+def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=16, lo=512, hi=16384):
+    rng = np.random.default_rng(5005)
+    lengths = rng.integers(lo, hi + 1, size=num_seqs).astype(np.int64)
+    final = lengths + steps
+    need = (final + bs - 1) // bs
+    num_blocks = int(need.sum()) + 64
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    max_blocks = int(need.max())
+    table = np.full((num_seqs, max_blocks), -1, np.int32)
+    pos = 0
+    for s in range(num_seqs):
+        table[s, : need[s]] = perm[pos: pos + need[s]]
+        pos += need[s]
+    row_elems = Hkv * D
+    pool_shape = (num_blocks, bs, Hkv, D)
+    dk = H.DeviceBuffer.from_array(bf16_bits(rng, pool_shape))
+    dv = H.DeviceBuffer.from_array(bf16_bits(rng, pool_shape))
+    dt = H.DeviceBuffer.from_array(table)
+    dq = H.DeviceBuffer.from_array(bf16_bits(rng, (num_seqs, Hq, 1, D)))
+    dout = H.DeviceBuffer(num_seqs * Hq * D * 2)
+    dlens = H.DeviceBuffer(num_seqs * 4)
+    parts = H.DeviceBuffer(4 * sca_amd.hip_lib().sca_hip_decode_partial_elements(num_seqs, Hq,
+                                                                                  splits, D))
+    new_k = H.DeviceBuffer.from_array(bf16_bits(rng, (num_seqs, Hkv, D)))
+    new_v = H.DeviceBuffer.from_array(bf16_bits(rng, (num_seqs, Hkv, D)))
+    dslots = H.DeviceBuffer(num_seqs * 4)
+    shape = H.KvShape()
+    shape.num_blocks, shape.block_size, shape.num_kv_heads, shape.head_dim = num_blocks, bs, Hkv, D
+    p = H.DecodeParams()
+    p.q, p.k, p.v, p.out = dq.ptr, dk.ptr, dv.ptr, dout.ptr
+    base = num_seqs * Hq * splits
+    p.partial_m, p.partial_l, p.partial_o = parts.ptr, parts.ptr + 4 * base, parts.ptr + 8 * base
+    p.batch, p.num_heads, p.num_kv_heads = num_seqs, Hq, Hkv
+    p.seq_kv, p.head_dim, p.num_splits = num_blocks * bs, D, splits
+    p.q_sb, p.q_sh = Hq * D, D
+    p.k_sb, p.k_sh, p.k_ss = 0, D, row_elems
+    p.v_sb, p.v_sh, p.v_ss = 0, D, row_elems
+    p.o_sb, p.o_sh = Hq * D, D
+    p.scale = float(np.float32(1.0 / np.sqrt(D)))
+    p.dtype = H.DTYPE_BF16
+    p.page_table, p.block_size, p.max_blocks_per_seq = dt.ptr, bs, max_blocks
+    p.num_kv_blocks, p.seq_lens = num_blocks, dlens.ptr
+    L = sca_amd.hip_lib()
+    cur = lengths.copy()
+    total_ms, total_bytes = 0.0, 0
+    start, stop = H.Event(), H.Event()
+    for step in range(steps + 2):  # two untimed warmup steps on the starting lengths
+        timed = step >= 2
+        if timed:
+            # append one token per sequence at position cur[s] (slot from the block table)
+            slots = (table[np.arange(num_seqs), cur // bs].astype(np.int64) * bs + cur % bs)
+            dslots.upload(slots.astype(np.int32))
+            H.check(L.sca_hip_kv_append(dk.ptr, dv.ptr, new_k.ptr, new_v.ptr, dslots.ptr,
+                                        num_seqs, shape, 2, None))
+            cur = cur + 1
+        dlens.upload(cur.astype(np.int32))
+        start.record()
+        H.decode_splitk_paged(p)
+        stop.record()
+        stop.synchronize()
+        if timed:
+            total_ms += start.elapsed_ms(stop)
+            total_bytes += int(cur.sum()) * Hkv * D * 2 * 2 + int(((cur + bs - 1) // bs).sum()) * 4 \
+                + 2 * num_seqs * Hq * D * 2
+    ms = total_ms / steps
+    nbytes = total_bytes / steps
+    return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9, "splits": splits,
+            "num_blocks": num_blocks, "pool_bytes": 2 * num_blocks * bs * row_elems * 2,
+            "mean_len": float(lengths.mean())}
+
+
+# ---- CPU baseline ------------------------------------------------------------------------------------
+def cpu_baseline(max_seconds=12.0):
+    import oracle.oracle as orc  # the CPU restatement is the timed baseline
+
+    threads = min(os.cpu_count() or 1, 16)
+    S, D = 4096, 128
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((1, 1, S, D), dtype=np.float32)
+    k = rng.standard_normal((1, 1, S, D), dtype=np.float32)
+    v = rng.standard_normal((1, 1, S, D), dtype=np.float32)
+    scores = np.empty(S * S, np.float32)
+    out = np.empty_like(q)
+    lse = np.empty((1, 1, S), np.float32)
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        orc.naive_attention_into(q, k, v, True, scale, scores, out, lse, threads)
+        runs += 1
+        if time.perf_counter() - t0 >= max_seconds or runs >= 50:
+            break
+    secs = (time.perf_counter() - t0) / runs
+    flops = causal_flops(1, 1, S, D)
+    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"naive 3-pass FP32 restatement (attention_naive.cu:41-135) on one head of "
+                      f"C2 (B=1,H=1,S=4096,D=128,causal), {runs} runs, {secs * 1e3:.1f} ms/run, "
+                      f"algorithmic causal FLOPs"}
+
+
+def load_traffic(name):
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--paged-steps", type=int, default=128)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["all", "prefill", "paged", "decode"], default="all")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              f"(this build has no multi-GPU path)", file=sys.stderr)
+        sys.exit(2)
+    if not sca_amd.gpu_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    probe = sca_amd.device_probe(0)
+
+    res = {}
+    if args.only in ("all", "prefill"):
+        res["c2_causal"] = bench_flash(args.steps, args.warmup, True)
+        res["c2_noncausal"] = bench_flash(args.steps, args.warmup, False)
+    if args.only in ("all", "paged"):
+        res["c5_paged"] = bench_paged(args.paged_steps)
+    if args.only in ("all", "decode"):
+        res["c4_decode"] = bench_decode(args.steps, args.warmup)
+
+    line = {
+        "metric": "prefill TFLOP/s (causal S=4096) + paged decode HBM GB/s, 1xMI355X",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic (seeded N(0,1))",
+        "device": {"name": probe.name.decode(), "arch": probe.arch_name.decode(),
+                   "cus": probe.cu_count},
+    }
+    if "c2_causal" in res:
+        c = res["c2_causal"]
+        line.update({"value": round(c["tflops"], 2), "unit": "TFLOP/s",
+                     "ms_per_step": round(c["ms"], 4)})
+        line["config"] = {"workload": "C2 flash prefill fp16 causal B=1 H=8 D=128 S=4096",
+                          "batch": 1, "heads": 8, "head_dim": 128, "seq_len": 4096,
+                          "causal": True}
+        line["roofline"] = {"bound": "mfma", "achieved": round(c["tflops"], 2),
+                            "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(c["tflops"] / PEAK_FP16_TFLOPS, 4),
+                            "traffic": load_traffic("flash_c2_causal")}
+        n = res["c2_noncausal"]
+        line["prefill_noncausal"] = {"value": round(n["tflops"], 2), "unit": "TFLOP/s",
+                                     "ms": round(n["ms"], 4),
+                                     "frac": round(n["tflops"] / PEAK_FP16_TFLOPS, 4)}
+    if "c5_paged" in res:
+        pg = res["c5_paged"]
+        line["paged_decode"] = {
+            "value": round(pg["gbps"], 1), "unit": "GB/s", "dtype": "bf16",
+            "ms_per_step": round(pg["ms"], 4), "steps": args.paged_steps,
+            "workload": "C5 paged decode bf16, 64 seqs L~U[512,16384], bs=16, Hq=32, Hkv=8, "
+                        "D=128, permuted block table, append 1 token/seq per step",
+            "roofline": {"bound": "hbm", "achieved": round(pg["gbps"], 1), "peak": PEAK_HBM_GBPS,
+                         "unit": "GB/s", "frac": round(pg["gbps"] / PEAK_HBM_GBPS, 4),
+                         "traffic": load_traffic("paged_c5")},
+        }
+    if "c4_decode" in res:
+        d = res["c4_decode"]
+        line["splitk_decode"] = {"value": round(d["gbps"], 1), "unit": "GB/s", "dtype": "f16",
+                                 "ms": round(d["ms"], 4), "splits": d["splits"],
+                                 "frac": round(d["gbps"] / PEAK_HBM_GBPS, 4)}
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
