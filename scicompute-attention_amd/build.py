@@ -86,7 +86,8 @@ def build_hip(workers: int) -> str:
     _compile_all(jobs, workers)
     out = os.path.join(LIB_DIR, "libsca_hip.so")
     tmp = out + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objects, "-o", tmp])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,--no-undefined", *objects, "-o",
+          tmp])
     os.replace(tmp, out)
     return out
 
@@ -106,7 +107,7 @@ def build_host(workers: int) -> str:
     out = os.path.join(LIB_DIR, "libsca_host.so")
     tmp = out + ".tmp"
     _run([CXX, "-shared", "-fPIC", *objects, "-o", tmp, "-L" + LIB_DIR, "-lsca_hip",
-          "-Wl,-rpath,$ORIGIN", "-pthread"])
+          "-Wl,-rpath,$ORIGIN", "-Wl,--no-undefined", "-pthread"])
     os.replace(tmp, out)
     return out
 

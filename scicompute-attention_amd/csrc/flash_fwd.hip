@@ -48,6 +48,7 @@ struct FlashGeom {
     static constexpr int WAVES = kRowGroups * KSPLIT;
     static constexpr int THREADS = WAVES * kWave;
     static constexpr int BN = 32 * KSPLIT;               // keys per tile
+    static constexpr int STAGES = 3;                     // LDS ring depth
     static constexpr int KS = D / 16;                    // QK k-steps
     static constexpr int DT = D / 32;                    // 32-row tiles of O^T
     static constexpr int KSTR = D + kKPad;               // K row stride (elements)
@@ -58,7 +59,7 @@ struct FlashGeom {
     static constexpr int V_PER_THREAD = (V_UNITS + THREADS - 1) / THREADS;
     static constexpr int K_STAGE = BN * KSTR;
     static constexpr int V_STAGE = D * VSTR;
-    static constexpr int STAGE_BYTES = 2 * (K_STAGE + V_STAGE) * 2;
+    static constexpr int STAGE_BYTES = STAGES * (K_STAGE + V_STAGE) * 2;
     static constexpr int MERGE_FLOATS = DT * 16 + 2;     // per lane: O^T + m + l
     static constexpr int MERGE_BYTES = KSPLIT > 1 ? kRowGroups * kWave * MERGE_FLOATS * 4 : 0;
     static constexpr int LDS_BYTES = STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES;
@@ -106,6 +107,11 @@ __device__ __forceinline__ uint32_t Half16(const uint4& v, int t) {
     return (t & 1) ? (w >> 16) : (w & 0xffffu);
 }
 
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedValu = 0x002;
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
 template <typename E, int D, bool kCausal>
 __global__ __launch_bounds__(FlashGeom<D>::THREADS, 1) void flash_fwd_kernel(
     const sca_flash_params p, int num_q_tiles) {
@@ -115,8 +121,8 @@ __global__ __launch_bounds__(FlashGeom<D>::THREADS, 1) void flash_fwd_kernel(
     constexpr int BN = G::BN;
 
     extern __shared__ __align__(16) uint16_t lds[];
-    uint16_t* sK = lds;                    // [2][BN][KSTR]
-    uint16_t* sV = lds + 2 * G::K_STAGE;   // [2][D][VSTR]  (V^T)
+    uint16_t* sK = lds;                           // [STAGES][BN][KSTR]
+    uint16_t* sV = lds + G::STAGES * G::K_STAGE;  // [STAGES][D][VSTR]  (V^T)
 
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
@@ -162,11 +168,16 @@ __global__ __launch_bounds__(FlashGeom<D>::THREADS, 1) void flash_fwd_kernel(
     }
 
     int n_tiles = (seq_kv + BN - 1) / BN;
+    // Tiles [0, n_plain) are inside seq_kv and fully visible to every row of the workgroup.
+    int n_plain = seq_kv / BN;
     if (kCausal) {
         const int last_key = q0 + kBlockM - 1 + diag;
         const int causal_tiles = last_key < 0 ? 0 : last_key / BN + 1;
         if (causal_tiles < n_tiles) n_tiles = causal_tiles;
+        const int plain = (q0 + diag + 1) / BN;
+        if (plain < n_plain) n_plain = plain;
     }
+    if (n_plain > n_tiles) n_plain = n_tiles;
 
     floatx16 o[G::DT];
 #pragma unroll
@@ -247,104 +258,134 @@ __global__ __launch_bounds__(FlashGeom<D>::THREADS, 1) void flash_fwd_kernel(
         }
     };
 
+    const int wkey_base = 32 * kh;  // this wave's first key inside a tile
+    const uint16_t* k_frag_base = sK + (wkey_base + lr) * G::KSTR + 8 * hh;
+    const uint16_t* v_frag_base = sV + lr * G::VSTR + wkey_base + 4 * hh;
+
+    // S^T[key][q] for this wave's 32 keys x 32 rows of the tile in `stage`.
+    auto qk = [&](int stage) {
+        const uint16_t* k_tile = k_frag_base + stage * G::K_STAGE;
+        vec8 a[G::KS];
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) a[ks] = *reinterpret_cast<const vec8*>(k_tile + 16 * ks);
+        floatx16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) s = M::mma(a[ks], qf[ks], s);
+        return s;
+    };
+
     if (n_tiles > 0) {
         load_tile(0);
         store_tile(0);
+        if (n_tiles > 1) {
+            load_tile(1);
+            store_tile(1);
+        }
     }
+    __syncthreads();
+    floatx16 s_cur = qk(0);
 
-    const int wkey_base = 32 * kh;  // this wave's first key inside a tile
-    for (int j = 0; j < n_tiles; ++j) {
-        __syncthreads();
-        const int stage = j & 1;
-        const bool more = (j + 1) < n_tiles;
-        if (more) load_tile(j + 1);
+    // One pipeline step. Tiles j and j+1 are resident in LDS, tile j+2 is being fetched:
+    //   region A: QK MFMAs of tile j+1 interleaved with the softmax VALU work of tile j;
+    //   O rescale (only when some lane's running max moved);
+    //   region C: PV MFMAs of tile j; then tile j+2 goes to LDS and the workgroup syncs.
+    auto step = [&]<bool kMask>(int j) {
+        if (j + 2 < n_tiles) load_tile(j + 2);
+        const int stage = j % G::STAGES;
+        const int next_stage = (j + 1) % G::STAGES;
 
-        const int wkey0 = j * BN + wkey_base;
-        // Skip the tile when none of this wave's 32 keys exists or is visible to its rows.
-        const bool wave_active = wkey0 < seq_kv &&
-                                 (!kCausal || wkey0 <= wave_q0 + kRowsPerWave - 1 + diag);
-        if (wave_active) {
-            const uint16_t* k_tile = sK + stage * G::K_STAGE + (wkey_base + lr) * G::KSTR + 8 * hh;
-            // S^T[key][q] for this wave's 32 keys x 32 rows.
-            floatx16 s;
+        // ---- region A (straight-line code) ----
+        floatx16 s_nxt = qk(next_stage);  // for the last tile this reads a stale stage; unused
+        floatx16 s = s_cur;
+        if constexpr (kMask) {
+            const int lim = kCausal ? min(seq_kv - 1, my_q + diag) : seq_kv - 1;
+            const int kbase = j * BN + wkey_base + 4 * hh;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[i] = 0.0f;
-#pragma unroll
-            for (int ks = 0; ks < G::KS; ++ks) {
-                const vec8 a = *reinterpret_cast<const vec8*>(k_tile + 16 * ks);
-                s = M::mma(a, qf[ks], s);
+            for (int i = 0; i < 16; ++i) {
+                const int key = kbase + 8 * (i / 4) + (i % 4);
+                s[i] = key > lim ? neg_inf() : s[i];
             }
-
-            // Mask only where some key is beyond seq_kv or above the causal diagonal.
-            const bool tail = wkey0 + 32 > seq_kv;
-            const bool on_diag = kCausal && (wkey0 + 31 > wave_q0 + diag);
-            if (tail || on_diag) {
-                const int lim = kCausal ? min(seq_kv - 1, my_q + diag) : seq_kv - 1;
+        }
+        float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
+                           fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+        tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(s[8], s[9]), fmaxf(s[10], s[11])),
+                                 fmaxf(fmaxf(s[12], s[13]), fmaxf(s[14], s[15]))));
+        tmax = fmaxf(tmax, xor32(tmax)) * scale2;
+        // Lazy rescale: the max used for the exponentials only moves when the row max grew by
+        // more than kRescaleSlack (weights stay <= 2^slack).
+        const bool grow = tmax > m_used + kRescaleSlack;
+        const float m_new = grow ? tmax : m_used;
+        const float alpha = grow ? fast_exp2(m_used - m_new) : 1.0f;
+        m_used = m_new;
+        l_run *= alpha;
+        const float mu = (m_used == neg_inf()) ? 0.0f : m_used;
+        uint32_t pw[8];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = wkey0 + 8 * (i / 4) + 4 * hh + (i % 4);
-                    if (key > lim) s[i] = neg_inf();
-                }
-            }
-
-            // Row max over the lane's 16 keys and the partner half (lane ^ 32).
-            float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
-                               fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-            tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(s[8], s[9]), fmaxf(s[10], s[11])),
-                                     fmaxf(fmaxf(s[12], s[13]), fmaxf(s[14], s[15]))));
-            tmax = fmaxf(tmax, xor32(tmax)) * scale2;
-            // Lazy rescale: the max used for the exponentials only moves when the row max grew by
-            // more than kRescaleSlack (weights stay <= 2^slack), and the O/l rescale runs only
-            // when some lane of the wave moved.
-            const bool grow = tmax > m_used + kRescaleSlack;
-            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-                const float m_new = grow ? tmax : m_used;
-                const float alpha = grow ? fast_exp2(m_used - m_new) : 1.0f;
-                m_used = m_new;
-                l_run *= alpha;
+        for (int i = 0; i < 8; ++i) {
+            const float p0 = fast_exp2(fmaf(s[2 * i], scale2, -mu));
+            const float p1 = fast_exp2(fmaf(s[2 * i + 1], scale2, -mu));
+            pw[i] = M::pack(p0, p1);
+            l_run = M::sum2(pw[i], l_run);
+        }
+        // Materialise P here: without this use the exponentials are sunk into region C, past
+        // the rescale branch, and no longer overlap the QK MFMAs.
 #pragma unroll
-                for (int dt = 0; dt < G::DT; ++dt) {
+        for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(pw[i]));
+        // interleave: K-fragment reads first, then one MFMA per ~12 VALU instructions
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, G::KS, 0);
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-                }
-            }
-            const float mu = (m_used == neg_inf()) ? 0.0f : m_used;
+        for (int i = 0; i < G::KS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedValu, 12, 0);
+        }
 
-            // P^T = 2^(s*scale2 - m), rounded to the input dtype: directly the PV B operand.
-            uint32_t pw[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float p0 = fast_exp2(fmaf(s[2 * i], scale2, -mu));
-                const float p1 = fast_exp2(fmaf(s[2 * i + 1], scale2, -mu));
-                pw[i] = M::pack(p0, p1);
-                l_run = M::sum2(pw[i], l_run);
-            }
-            const vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-            const vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
-
-            // O^T[d][q] += V^T[d][key] P^T[key][q]; k-step ps covers keys
-            // 16*ps + {0..3, 8..11} (hh = 0) or 16*ps + {4..7, 12..15} (hh = 1).
-            const uint16_t* v_tile =
-                sV + stage * G::V_STAGE + lr * G::VSTR + wkey_base + 4 * hh;
+        // ---- O rescale (rare) ----
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
             for (int dt = 0; dt < G::DT; ++dt) {
 #pragma unroll
-                for (int ps = 0; ps < 2; ++ps) {
-                    const uint16_t* vrow = v_tile + 32 * dt * G::VSTR + 16 * ps;
-                    const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
-                    const vec8 a = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                    o[dt] = M::mma(a, ps == 0 ? pb0 : pb1, o[dt]);
-                }
+                for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
             }
         }
 
-        if (more) store_tile((j + 1) & 1);
-    }
+        // ---- region C: O^T[d][q] += V^T[d][key] P^T[key][q] ----
+        // k-step ps covers keys 16*ps + {0..3, 8..11} (hh = 0) or 16*ps + {4..7, 12..15} (hh = 1).
+        const vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+        const vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
+        const uint16_t* v_tile = v_frag_base + stage * G::V_STAGE;
+        vec8 va[G::DT][2];
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+            for (int ps = 0; ps < 2; ++ps) {
+                const uint16_t* vrow = v_tile + 32 * dt * G::VSTR + 16 * ps;
+                const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+                va[dt][ps] = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+            o[dt] = M::mma(va[dt][0], pb0, o[dt]);
+            o[dt] = M::mma(va[dt][1], pb1, o[dt]);
+        }
+        // all V^T fragment reads in flight before the first PV MFMA
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * G::DT, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * G::DT, 0);
+
+        if (j + 2 < n_tiles) store_tile((j + 2) % G::STAGES);
+        __syncthreads();
+        s_cur = s_nxt;
+    };
+
+    int j = 0;
+    for (; j < n_plain; ++j) step.template operator()<false>(j);
+    for (; j < n_tiles; ++j) step.template operator()<true>(j);
 
     // Merge the KSPLIT partial states of each row group through LDS.
     if constexpr (G::KSPLIT > 1) {
-        __syncthreads();  // every wave is done reading the K/V stages
         float* mbuf = reinterpret_cast<float*>(lds) + (rg * kWave + lane) * G::MERGE_FLOATS;
         if (kh == 1) {
 #pragma unroll
@@ -394,6 +435,458 @@ __global__ __launch_bounds__(FlashGeom<D>::THREADS, 1) void flash_fwd_kernel(
     }
 }
 
+// ============================================================================================
+// DMA-pipelined variant for head_dim 64 and 128 (the serving shapes).
+//
+// K and V tiles go straight from global memory to LDS with global_load_lds_dwordx4 (no VGPR
+// staging, no transposition), through a 4-stage ring whose loads are issued two tiles ahead of
+// their use and retired with explicit vmcnt waits. LDS rows are unpadded; 16-byte chunks are
+// XOR-swizzled (K: chunk ^ (row % 8), V: chunk ^ 4*(row & 1)) so that both the K reads and the V
+// transpose reads are bank-conflict free. The PV A operand (V^T fragments) comes from
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j % 4 of the 8 bytes
+// read by lane 4*i + j/4 (i = 0..3), i.e. one head-dim column over 4 consecutive keys.
+// ============================================================================================
+template <int D>
+struct DmaGeom {
+    static constexpr int BN = 64;                 // keys per tile (2 waves x 32 keys per row group)
+    static constexpr int WAVES = 8;
+    static constexpr int THREADS = WAVES * kWave;
+    static constexpr int STAGES = 4;
+    static constexpr int KS = D / 16;
+    static constexpr int DT = D / 32;
+    static constexpr int CPR = D / 8;             // 16-byte chunks per row
+    static constexpr int TILE_BYTES = BN * D * 2; // one K or V tile
+    static constexpr int STAGE_BYTES = 2 * TILE_BYTES;
+    static constexpr int IPW = BN * CPR / kWave / WAVES;  // DMA instructions per wave per tile
+    static constexpr int LOADS_PER_TILE = 2 * IPW;        // K + V, per wave
+    static constexpr int MERGE_FLOATS = DT * 16 + 2;
+    static constexpr int MERGE_BYTES = kRowGroups * kWave * MERGE_FLOATS * 4;
+    static constexpr int RING_BYTES = STAGES * STAGE_BYTES;
+    static constexpr int LDS_BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
+    static_assert(IPW >= 1 && BN * CPR == IPW * kWave * WAVES, "tile must split evenly into DMAs");
+};
+
+// 16-byte-chunk swizzles for 64 LDS banks (a 256-byte bank window):
+//   K: the 32 rows a wave reads in one ds_read_b128 land on 16 distinct 4-bank groups;
+//   V: the 8 keys x 4 chunks of one transpose read land on 16 distinct groups.
+template <int D>
+__device__ __forceinline__ int SwzK(int row) {
+    return D == 128 ? (row & 15) : ((row >> 1) & 7);
+}
+template <int D>
+__device__ __forceinline__ int SwzV(int row) {
+    return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
+}
+
+// (lower-half value, upper-half value) of v for lanes l and l ^ 32, on every lane, from one
+// v_permlane32_swap: it exchanges the upper 32 lanes of its first operand with the lower 32 lanes
+// of its second, so with both operands holding v the first ends as (v_lo, v_lo) and the second as
+// (v_hi, v_hi). Issued from inline asm with both registers as in/out operands (the builtin's
+// second result is not reliably kept apart from the first), after the two wait states a VALU
+// write needs before the permlane reads it.
+__device__ __forceinline__ void HalfPair(float v, float* lo, float* hi) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v);
+    uint32_t b = a;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    *lo = __builtin_bit_cast(float, a);
+    *hi = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float HalfMax(float v) {
+    float lo, hi;
+    HalfPair(v, &lo, &hi);
+    return fmaxf(lo, hi);
+}
+__device__ __forceinline__ float HalfSum(float v) {
+    float lo, hi;
+    HalfPair(v, &lo, &hi);
+    return lo + hi;
+}
+
+template <typename E>
+struct TrRead;
+
+template <>
+struct TrRead<F16> {
+    typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 v4;
+    static __device__ __forceinline__ uint2 read(const uint8_t* lds_byte_ptr) {
+        const v4 r = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (__attribute__((address_space(3))) v4*)(lds_byte_ptr));
+        return __builtin_bit_cast(uint2, r);
+    }
+};
+
+template <>
+struct TrRead<BF16> {
+    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 v4;
+    static __device__ __forceinline__ uint2 read(const uint8_t* lds_byte_ptr) {
+        const v4 r = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (__attribute__((address_space(3))) v4*)(lds_byte_ptr));
+        return __builtin_bit_cast(uint2, r);
+    }
+};
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt bits [3:0] and [15:14]).
+template <int N>
+__device__ __forceinline__ void WaitVm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// 16-byte DMA of lane data from a raw buffer (base, num_records) at voffset + soffset into LDS
+// at lds + 16 * lane. Bytes at or beyond num_records read as zero. (The buffer resource is
+// built here rather than in the kernel body: a buffer-resource local in a kernel body makes the
+// host pass drop the kernel's launch stub.)
+__device__ __forceinline__ void DmaToLds(const uint8_t* base, int num_records, uint8_t* lds,
+                                         uint32_t voffset, uint32_t soffset) {
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(base), 0, num_records, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds), 16,
+                                             voffset, soffset, 0, 0);
+}
+
+template <typename E, int D, bool kCausal>
+__global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
+    const sca_flash_params p, int num_q_tiles) {
+    using G = DmaGeom<D>;
+    using M = Mfma<E>;
+    using vec8 = typename E::vec8;
+    constexpr int BN = G::BN;
+    constexpr int ROW_BYTES = D * 2;
+    static_assert(2 * G::STAGE_BYTES <= 65536, "stage offsets must fit the 16-bit DS immediate");
+
+    extern __shared__ __align__(16) uint8_t lds8[];
+    // Stages 0/1 are addressed from lds8, stages 2/3 from lds8 + 2 stages; within each half the
+    // stage offset is a DS immediate.
+    uint8_t* const lds_hi = lds8 + 2 * G::STAGE_BYTES;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int lane = tid % kWave;
+    const int lr = lane & 31;
+    const int hh = lane >> 5;
+    const int rg = wave % kRowGroups;
+    const int kh = wave / kRowGroups;
+
+    const int64_t bh_count = p.batch * p.num_heads;
+    const int64_t tile_linear = static_cast<int64_t>(blockIdx.x) / bh_count;
+    const int64_t bh = static_cast<int64_t>(blockIdx.x) % bh_count;
+    const int64_t qt = kCausal ? (num_q_tiles - 1 - tile_linear) : tile_linear;
+    const int64_t b = bh / p.num_heads;
+    const int64_t h = bh % p.num_heads;
+    const int64_t h_kv = h / (p.num_heads / p.num_kv_heads);
+    const int q0 = static_cast<int>(qt) * kBlockM;
+    const int wave_q0 = q0 + rg * kRowsPerWave;
+    const int my_q = wave_q0 + lr;
+    const int seq_q = static_cast<int>(p.seq_q);
+    const int seq_kv = static_cast<int>(p.seq_kv);
+    const int diag = static_cast<int>(p.diagonal);
+
+    const uint16_t* q_ptr = static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh;
+    const uint8_t* k_bytes =
+        reinterpret_cast<const uint8_t*>(static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh);
+    const uint8_t* v_bytes =
+        reinterpret_cast<const uint8_t*>(static_cast<const uint16_t*>(p.v) + b * p.v_sb + h_kv * p.v_sh);
+    const int k_row_bytes = static_cast<int>(p.k_ss) * 2;
+    const int v_row_bytes = static_cast<int>(p.v_ss) * 2;
+
+    vec8 qf[G::KS];
+    {
+        const uint16_t* q_row = q_ptr + static_cast<int64_t>(my_q) * p.q_ss + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+            uint4 raw = make_uint4(0, 0, 0, 0);
+            if (my_q < seq_q) raw = *reinterpret_cast<const uint4*>(q_row + 16 * ks);
+            qf[ks] = __builtin_bit_cast(vec8, raw);
+        }
+        WaitVm<0>();  // Q is in registers before any tile DMA is counted
+    }
+
+    int n_tiles = (seq_kv + BN - 1) / BN;
+    int n_plain = seq_kv / BN;
+    if (kCausal) {
+        const int last_key = q0 + kBlockM - 1 + diag;
+        const int causal_tiles = last_key < 0 ? 0 : last_key / BN + 1;
+        if (causal_tiles < n_tiles) n_tiles = causal_tiles;
+        const int plain = (q0 + diag + 1) / BN;
+        if (plain < n_plain) n_plain = plain;
+    }
+    if (n_plain > n_tiles) n_plain = n_tiles;
+
+    // ---- DMA through buffer resources: base = this (b, kv head), num_records covers the rows
+    //      that exist, so rows past seq_kv (tail tile, or tiles past the end) read as zero and
+    //      need no clamping; every wave issues the same number of DMAs per tile.
+    //      Instruction i of this wave fills bytes [(wave*IPW + i)*1024, +1024) of a tile; lane L
+    //      brings flat chunk P = (wave*IPW + i)*64 + L, i.e. row P / CPR, position P % CPR, which
+    //      holds logical chunk position ^ swizzle(row).
+    const int k_records = (seq_kv - 1) * k_row_bytes + ROW_BYTES;
+    const int v_records = (seq_kv - 1) * v_row_bytes + ROW_BYTES;
+    uint32_t dma_koff[G::IPW], dma_voff[G::IPW];
+#pragma unroll
+    for (int i = 0; i < G::IPW; ++i) {
+        const int P = (wave * G::IPW + i) * kWave + lane;
+        const int row = P / G::CPR;
+        const int pos = P % G::CPR;
+        dma_koff[i] = row * k_row_bytes + (pos ^ SwzK<D>(row)) * 16;
+        dma_voff[i] = row * v_row_bytes + (pos ^ SwzV<D>(row)) * 16;
+    }
+
+    auto issue_tile = [&]<int S>(int t) {
+        uint8_t* k_dst = lds8 + S * G::STAGE_BYTES + wave * G::IPW * 1024;
+        uint8_t* v_dst = k_dst + G::TILE_BYTES;
+        const uint32_t k_tile_off = static_cast<uint32_t>(t * BN * k_row_bytes);
+        const uint32_t v_tile_off = static_cast<uint32_t>(t * BN * v_row_bytes);
+#pragma unroll
+        for (int i = 0; i < G::IPW; ++i) {
+            DmaToLds(k_bytes, k_records, k_dst + i * 1024, dma_koff[i], k_tile_off);
+        }
+#pragma unroll
+        for (int i = 0; i < G::IPW; ++i) {
+            DmaToLds(v_bytes, v_records, v_dst + i * 1024, dma_voff[i], v_tile_off);
+        }
+    };
+
+    floatx16 o[G::DT];
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
+    }
+    float m_used = neg_inf();
+    float l_run = 0.0f;
+    const float scale2 = p.scale * kLog2e;
+
+    const int wkey_base = 32 * kh;
+    // K fragment of k-step ks: row wkey_base + lr, logical chunk 2*ks + hh (= 2*ks ^ hh).
+    const int k_row = wkey_base + lr;
+    uint32_t k_frag[G::KS];
+#pragma unroll
+    for (int ks = 0; ks < G::KS; ++ks) {
+        k_frag[ks] = k_row * ROW_BYTES + (((2 * ks) ^ hh ^ SwzK<D>(k_row)) * 16);
+    }
+    // V^T transpose read of (dt, ps, r): source key v_key + 16*ps + 8*r, head-dim chunk
+    // 4*dt + v_chunk (swizzled), half v_half. The swizzle only depends on key bits the
+    // (16*ps + 8*r) step does not touch, so each dt has one lane offset.
+    const int grp = lane >> 4;
+    const int sl = lane & 15;
+    const int v_key = wkey_base + 4 * hh + (sl >> 2);
+    const int v_chunk = 2 * (grp & 1) + ((sl & 3) >> 1);
+    const int v_half = (sl & 1) * 8;
+    uint32_t v_frag[G::DT];
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt) {
+        v_frag[dt] = G::TILE_BYTES + v_key * ROW_BYTES + (((4 * dt + v_chunk) ^ SwzV<D>(v_key)) * 16) +
+                     v_half;
+    }
+
+    auto qk = [&]<int S>() {
+        const uint8_t* base = (S < 2 ? lds8 : lds_hi) + (S & 1) * G::STAGE_BYTES;
+        vec8 a[G::KS];
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) a[ks] = *reinterpret_cast<const vec8*>(base + k_frag[ks]);
+        floatx16 acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) acc = M::mma(a[ks], qf[ks], acc);
+        return acc;
+    };
+
+    // One pipeline step for tile j (held in stage S; tile j+1 in stage S+1, tiles j+2 and j+3
+    // in flight): QK MFMAs of tile j+1 interleaved with the softmax VALU of tile j, the O rescale
+    // when some lane's running max moved, PV MFMAs of tile j, then retire tile j+2 and sync.
+    auto step = [&]<bool kMask, int S>(int j, floatx16& s_in, floatx16& s_out) {
+        issue_tile.template operator()<(S + 3) & 3>(j + 3);
+        s_out = qk.template operator()<(S + 1) & 3>();
+        floatx16 sv = s_in;
+        if constexpr (kMask) {
+            const int lim = kCausal ? min(seq_kv - 1, my_q + diag) : seq_kv - 1;
+            const int kbase = j * BN + wkey_base + 4 * hh;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kbase + 8 * (i / 4) + (i % 4);
+                sv[i] = key > lim ? neg_inf() : sv[i];
+            }
+        }
+        float tmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                           fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(sv[8], sv[9]), fmaxf(sv[10], sv[11])),
+                                 fmaxf(fmaxf(sv[12], sv[13]), fmaxf(sv[14], sv[15]))));
+        tmax = HalfMax(tmax) * scale2;
+        const bool grow = tmax > m_used + kRescaleSlack;
+        const float m_new = grow ? tmax : m_used;
+        const float alpha = grow ? fast_exp2(m_used - m_new) : 1.0f;
+        m_used = m_new;
+        l_run *= alpha;
+        const float mu = (m_used == neg_inf()) ? 0.0f : m_used;
+        uint32_t pw[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float p0 = fast_exp2(fmaf(sv[2 * i], scale2, -mu));
+            const float p1 = fast_exp2(fmaf(sv[2 * i + 1], scale2, -mu));
+            pw[i] = M::pack(p0, p1);
+            l_run = M::sum2(pw[i], l_run);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(pw[i]));
+        // K fragments in two halves (bounds the live registers), MFMAs spread over the VALU work
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, G::KS / 2, 0);
+#pragma unroll
+        for (int i = 0; i < G::KS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedValu, 10, 0);
+            if (i == 0) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, G::KS - G::KS / 2, 0);
+        }
+
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+            for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+            }
+        }
+
+        const vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+        const vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
+        const uint8_t* vbase = (S < 2 ? lds8 : lds_hi) + (S & 1) * G::STAGE_BYTES;
+        vec8 va[G::DT][2];
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+            for (int ps = 0; ps < 2; ++ps) {
+                const uint2 lo = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps) * ROW_BYTES);
+                const uint2 hi = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps + 8) * ROW_BYTES);
+                va[dt][ps] = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+            o[dt] = M::mma(va[dt][0], pb0, o[dt]);
+            o[dt] = M::mma(va[dt][1], pb1, o[dt]);
+        }
+        // V^T fragments for two O tiles at a time ahead of their MFMAs
+#pragma unroll
+        for (int dt = 0; dt < G::DT; dt += 2) {
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+        }
+
+        // Tile j+2 has landed (tile j+3 may still be in flight); publish it, and make sure every
+        // wave is done with stage S before it is refilled by the next step.
+        WaitVm<G::LOADS_PER_TILE>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+    };
+
+    issue_tile.template operator()<0>(0);
+    issue_tile.template operator()<1>(1);
+    issue_tile.template operator()<2>(2);
+    WaitVm<G::LOADS_PER_TILE>();  // tiles 0 and 1 landed (tile 2 may be in flight)
+    __builtin_amdgcn_s_barrier();
+    floatx16 s0 = qk.template operator()<0>();
+    floatx16 s1;
+
+    int j = 0;
+    // Steady state: four steps per trip, stages fixed at compile time, scores ping-pong s0/s1.
+    for (; j + 4 <= n_plain; j += 4) {
+        step.template operator()<false, 0>(j, s0, s1);
+        step.template operator()<false, 1>(j + 1, s1, s0);
+        step.template operator()<false, 2>(j + 2, s0, s1);
+        step.template operator()<false, 3>(j + 3, s1, s0);
+    }
+    // Remaining plain tiles and the boundary tiles (masking a fully visible tile is harmless).
+    for (; j < n_tiles; ++j) {
+        switch (j & 3) {
+            case 0: step.template operator()<true, 0>(j, s0, s1); break;
+            case 1: step.template operator()<true, 1>(j, s0, s1); break;
+            case 2: step.template operator()<true, 2>(j, s0, s1); break;
+            default: step.template operator()<true, 3>(j, s0, s1); break;
+        }
+        s0 = s1;
+    }
+
+    // Drain the trailing DMAs before the LDS is reused for the merge (or released).
+    WaitVm<0>();
+    __builtin_amdgcn_s_barrier();
+
+    {
+        float* mbuf = reinterpret_cast<float*>(lds8) + (rg * kWave + lane) * G::MERGE_FLOATS;
+        if (kh == 1) {
+#pragma unroll
+            for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mbuf[dt * 16 + i] = o[dt][i];
+            }
+            mbuf[G::DT * 16] = m_used;
+            mbuf[G::DT * 16 + 1] = l_run;
+        }
+        __syncthreads();
+        if (kh == 1) return;
+        const float m_o = mbuf[G::DT * 16];
+        const float l_o = mbuf[G::DT * 16 + 1];
+        const float mm = fmaxf(m_used, m_o);
+        const float wa = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
+        const float wb = (m_o == neg_inf()) ? 0.0f : fast_exp2(m_o - mm);
+        m_used = mm;
+        l_run = l_run * wa + l_o * wb;
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[dt][i] = o[dt][i] * wa + mbuf[dt * 16 + i] * wb;
+        }
+    }
+
+    const float l_tot = HalfSum(l_run);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (my_q < seq_q) {
+        uint16_t* out_row = static_cast<uint16_t*>(p.out) + b * p.o_sb + h * p.o_sh +
+                            static_cast<int64_t>(my_q) * p.o_ss;
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d0 = 32 * dt + 8 * g + 4 * hh;
+                const uint32_t lo = M::pack(o[dt][4 * g + 0] * inv, o[dt][4 * g + 1] * inv);
+                const uint32_t hi = M::pack(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+                *reinterpret_cast<uint2*>(out_row + d0) = make_uint2(lo, hi);
+            }
+        }
+        if (p.lse != nullptr && hh == 0) {
+            p.lse[(b * p.num_heads + h) * p.seq_q + my_q] =
+                l_tot > 0.0f ? (m_used + __log2f(l_tot)) * kLn2 : neg_inf();
+        }
+    }
+}
+
+template <typename E, int D, bool kCausal>
+int LaunchFlash(const sca_flash_params& p, hipStream_t s);
+
+template <typename E, int D, bool kCausal>
+int LaunchFlashDma(const sca_flash_params& p, hipStream_t s) {
+    using G = DmaGeom<D>;
+    // Buffer offsets are 32-bit: rows up to seq_kv plus a few tiles of overrun must fit.
+    const int64_t extent_k = (p.seq_kv + 4 * G::BN) * p.k_ss * 2;
+    const int64_t extent_v = (p.seq_kv + 4 * G::BN) * p.v_ss * 2;
+    if (extent_k >= (1LL << 31) || extent_v >= (1LL << 31)) return LaunchFlash<E, D, kCausal>(p, s);
+    const int64_t num_q_tiles = (p.seq_q + kBlockM - 1) / kBlockM;
+    const int64_t blocks = num_q_tiles * p.batch * p.num_heads;
+    if (blocks <= 0) return 0;
+    if (blocks > 0x7fffffffLL) {
+        return SetError(SCA_E_SEQ_TOO_LONG, "flash: grid of " + std::to_string(blocks) +
+                                                " workgroups exceeds the launch limit");
+    }
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t err = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&flash_fwd_dma_kernel<E, D, kCausal>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
+        if (err != hipSuccess) (void)hipGetLastError();
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((flash_fwd_dma_kernel<E, D, kCausal>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(G::THREADS), G::LDS_BYTES, s, p, static_cast<int>(num_q_tiles));
+    return CheckLaunch("flash_fwd_dma_kernel", s);
+}
+
 template <typename E, int D, bool kCausal>
 int LaunchFlash(const sca_flash_params& p, hipStream_t s) {
     using G = FlashGeom<D>;
@@ -423,9 +916,9 @@ template <typename E, bool kCausal>
 int LaunchForDim(const sca_flash_params& p, hipStream_t s) {
     switch (p.head_dim) {
         case 32: return LaunchFlash<E, 32, kCausal>(p, s);
-        case 64: return LaunchFlash<E, 64, kCausal>(p, s);
+        case 64: return LaunchFlashDma<E, 64, kCausal>(p, s);
         case 96: return LaunchFlash<E, 96, kCausal>(p, s);
-        case 128: return LaunchFlash<E, 128, kCausal>(p, s);
+        case 128: return LaunchFlashDma<E, 128, kCausal>(p, s);
         case 160: return LaunchFlash<E, 160, kCausal>(p, s);
         case 192: return LaunchFlash<E, 192, kCausal>(p, s);
         case 256: return LaunchFlash<E, 256, kCausal>(p, s);
@@ -440,9 +933,9 @@ bool Aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 int LdsBytesFor(int64_t head_dim) {
     switch (head_dim) {
         case 32: return FlashGeom<32>::LDS_BYTES;
-        case 64: return FlashGeom<64>::LDS_BYTES;
+        case 64: return DmaGeom<64>::LDS_BYTES;
         case 96: return FlashGeom<96>::LDS_BYTES;
-        case 128: return FlashGeom<128>::LDS_BYTES;
+        case 128: return DmaGeom<128>::LDS_BYTES;
         case 160: return FlashGeom<160>::LDS_BYTES;
         case 192: return FlashGeom<192>::LDS_BYTES;
         case 256: return FlashGeom<256>::LDS_BYTES;
