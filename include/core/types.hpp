@@ -9,6 +9,13 @@
 #include <initializer_list>
 #include <vector>
 
+// Visibility of the sci:: infrastructure symbols exported by libsca_host.so.
+#if defined(__GNUC__) || defined(__clang__)
+#define SCI_INFRA_API __attribute__((visibility("default")))
+#else
+#define SCI_INFRA_API
+#endif
+
 namespace sci {
 
 using index_t = int64_t;

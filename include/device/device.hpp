@@ -19,7 +19,7 @@ namespace sci {
 
 class Stream;
 
-class Device {
+class SCI_INFRA_API Device {
 public:
     virtual ~Device() = default;
     virtual DeviceType type() const = 0;
@@ -38,17 +38,17 @@ public:
 };
 
 // Process-wide CPU device.
-Device& HostDevice();
+SCI_INFRA_API Device& HostDevice();
 
 // Process-wide HIP device `id`. Callers should check GpuAvailable() first: on a machine without a
 // GPU the returned device fails every allocation (allocate returns nullptr).
-Device& GpuDevice(int id = 0);
-bool GpuAvailable();
+SCI_INFRA_API Device& GpuDevice(int id = 0);
+SCI_INFRA_API bool GpuAvailable();
 
 // Releases every block cached by GpuDevice(id)'s pool; returns the number of bytes released.
-size_t GpuEmptyCache(int id = 0);
+SCI_INFRA_API size_t GpuEmptyCache(int id = 0);
 // Bytes currently cached (not handed out) and bytes handed out by GpuDevice(id)'s pool.
-size_t GpuCachedBytes(int id = 0);
-size_t GpuAllocatedBytes(int id = 0);
+SCI_INFRA_API size_t GpuCachedBytes(int id = 0);
+SCI_INFRA_API size_t GpuAllocatedBytes(int id = 0);
 
 }  // namespace sci

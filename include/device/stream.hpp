@@ -10,7 +10,7 @@
 
 namespace sci {
 
-class Stream {
+class SCI_INFRA_API Stream {
 public:
     Stream() = default;
     explicit Stream(void* handle) : handle_(handle) {}

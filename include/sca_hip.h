@@ -220,6 +220,14 @@ SCA_HIP_API int sca_hip_kv_gather(const void* layer, const int32_t* block_ids,
                                   int64_t num_block_ids, void* out, const sca_kv_shape* shape,
                                   int64_t elem_bytes, void* stream);
 
+/* Sparse int32 update: dst[pairs[2i]] = pairs[2i+1] for i < num_pairs (indices outside
+ * [0, dst_len) are skipped; pairs 8 B aligned, device). Used to refresh only the changed entries
+ * of a device page table.
+ * replaces: the whole-table re-upload of src/kv_cache/paged_kv_cache.cpp:182-201 (no kernel
+ *           counterpart in the reference) */
+SCA_HIP_API int sca_hip_i32_scatter(int32_t* dst, int64_t dst_len, const int32_t* pairs,
+                                    int64_t num_pairs, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

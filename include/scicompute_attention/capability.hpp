@@ -12,7 +12,7 @@ namespace sca {
 // What the GPU offers, probed once per device through the kernel library's C ABI and cached
 // (Refresh() re-probes). Field names follow the reference's struct so that caller code compiles
 // unchanged; on CDNA "sm" means compute unit and "smem" means LDS.
-struct DeviceCapability {
+struct SCI_ATTENTION_API DeviceCapability {
     std::string device_name;
     std::string arch_name;               // e.g. "gfx950:sramecc+:xnack-"
     int major{0};

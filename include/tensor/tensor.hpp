@@ -14,7 +14,7 @@
 
 namespace sci {
 
-class Tensor {
+class SCI_INFRA_API Tensor {
 public:
     Tensor() = default;
     Tensor(const TensorShape& shape, DType dtype, Device& device);

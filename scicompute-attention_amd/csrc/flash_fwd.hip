@@ -961,10 +961,31 @@ int sca_hip_flash_tile(int32_t head_dim, int32_t* block_m, int32_t* block_n, int
         return SetError(SCA_E_UNSUPPORTED_HEAD_DIM,
                         "flash: no tile for head_dim=" + std::to_string(head_dim));
     }
+    // D = 64 / 128 run the DMA-fed kernel; the other head dims the register-staged one.
+    const bool dma = head_dim == 64 || head_dim == 128;
+    int32_t bn = 0, nw = 0, ns = 0;
+    switch (head_dim) {
+        case 32: bn = sca_hip::FlashGeom<32>::BN; nw = sca_hip::FlashGeom<32>::WAVES;
+                 ns = sca_hip::FlashGeom<32>::STAGES; break;
+        case 96: bn = sca_hip::FlashGeom<96>::BN; nw = sca_hip::FlashGeom<96>::WAVES;
+                 ns = sca_hip::FlashGeom<96>::STAGES; break;
+        case 160: bn = sca_hip::FlashGeom<160>::BN; nw = sca_hip::FlashGeom<160>::WAVES;
+                  ns = sca_hip::FlashGeom<160>::STAGES; break;
+        case 192: bn = sca_hip::FlashGeom<192>::BN; nw = sca_hip::FlashGeom<192>::WAVES;
+                  ns = sca_hip::FlashGeom<192>::STAGES; break;
+        case 256: bn = sca_hip::FlashGeom<256>::BN; nw = sca_hip::FlashGeom<256>::WAVES;
+                  ns = sca_hip::FlashGeom<256>::STAGES; break;
+        default: break;
+    }
+    if (dma) {
+        bn = sca_hip::DmaGeom<64>::BN;
+        nw = sca_hip::DmaGeom<64>::WAVES;
+        ns = sca_hip::DmaGeom<64>::STAGES;
+    }
     if (block_m != nullptr) *block_m = sca_hip::kBlockM;
-    if (block_n != nullptr) *block_n = head_dim <= 128 ? 64 : 32;
-    if (waves != nullptr) *waves = head_dim <= 128 ? 8 : 4;
-    if (stages != nullptr) *stages = 2;
+    if (block_n != nullptr) *block_n = bn;
+    if (waves != nullptr) *waves = nw;
+    if (stages != nullptr) *stages = ns;
     return 0;
 }
 

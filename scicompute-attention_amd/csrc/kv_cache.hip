@@ -67,6 +67,17 @@ __global__ void kv_gather_kernel(const uint4* __restrict__ layer, const int32_t*
     }
 }
 
+// dst[pairs[2i]] = pairs[2i+1]; indices outside [0, dst_len) are skipped.
+__global__ void i32_scatter_kernel(int32_t* __restrict__ dst, int64_t dst_len,
+                                   const int2* __restrict__ pairs, int64_t num_pairs) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < num_pairs;
+         i += stride) {
+        const int2 pr = pairs[i];
+        if (pr.x >= 0 && pr.x < dst_len) dst[pr.x] = pr.y;
+    }
+}
+
 unsigned GridFor(int64_t total) {
     int64_t blocks = (total + kThreads - 1) / kThreads;
     if (blocks < 1) blocks = 1;
@@ -170,6 +181,22 @@ int sca_hip_kv_gather(const void* layer, const int32_t* block_ids, int64_t num_b
                        dim3(sca_hip::kThreads), 0, s, static_cast<const uint4*>(layer), block_ids,
                        num_block_ids, static_cast<uint4*>(out), block_chunks, shape->num_blocks);
     return sca_hip::CheckLaunch("kv_gather_kernel", s);
+}
+
+int sca_hip_i32_scatter(int32_t* dst, int64_t dst_len, const int32_t* pairs, int64_t num_pairs,
+                        void* stream) {
+    if (num_pairs <= 0) return 0;
+    if (dst == nullptr || pairs == nullptr) {
+        return SetError(SCA_E_SHAPE_MISMATCH, "i32_scatter: null pointer");
+    }
+    if ((reinterpret_cast<uintptr_t>(pairs) & 7u) != 0) {
+        return SetError(SCA_E_LAYOUT_MISMATCH, "i32_scatter: pairs must be 8 B aligned");
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(sca_hip::i32_scatter_kernel, dim3(sca_hip::GridFor(num_pairs)),
+                       dim3(sca_hip::kThreads), 0, s, dst, dst_len,
+                       reinterpret_cast<const int2*>(pairs), num_pairs);
+    return sca_hip::CheckLaunch("i32_scatter_kernel", s);
 }
 
 }  // extern "C"

@@ -28,3 +28,5 @@ from .hip import (  # noqa: F401
     device_probe,
     synchronize,
 )
+
+from . import host  # noqa: E402,F401  (libsca_host.so is loaded lazily by host.host_lib())

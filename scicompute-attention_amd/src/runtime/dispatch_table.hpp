@@ -1,0 +1,54 @@
+// Compiled-in dispatch thresholds of the MI355X build.
+//
+// The routing rules are the reference's (src/runtime/dispatch_table.inc:30-37, r0) except one:
+// short sequences (seq_kv <= 128) go to the flash kernel, which serves every length without a
+// score workspace, instead of the reference's score-materialising tiled kernel (not built here).
+// Split counts are derived from the compute-unit count: enough workgroups for every CU to hold
+// several, each split still covering at least `min_tokens_per_split` keys.
+#pragma once
+
+#include <cstdint>
+
+namespace sca {
+namespace detail {
+
+struct DispatchThresholds {
+    int64_t decode_max_seq_q;      // seq_q <= this and seq_kv >= decode_min_seq_kv => decode
+    int64_t decode_min_seq_kv;
+    int64_t short_max_seq_kv;      // seq_kv <= this => "short sequence" rule (flash here)
+    int64_t min_tokens_per_split;  // lower bound on keys per split
+    int64_t workgroups_per_cu;     // split-K target occupancy
+    int64_t max_splits;            // cap on the split count (explicit and automatic)
+    const char* revision;          // reported by Explain()
+};
+
+inline constexpr DispatchThresholds kDispatchThresholds{
+    /* decode_max_seq_q     */ 1,
+    /* decode_min_seq_kv    */ 256,
+    /* short_max_seq_kv     */ 128,
+    /* min_tokens_per_split */ 256,
+    /* workgroups_per_cu    */ 4,
+    /* max_splits           */ 64,
+    /* revision             */ "r0-mi355x",
+};
+
+// Split count of the decode kernels for `batch` sequences of up to `seq_kv` keys. The kernel runs
+// one workgroup per (sequence, KV head, split) and serves the whole GQA group of a KV head when
+// the group size is a multiple of 8, 4 or 2 (smaller groups need several workgroups per KV head).
+inline int64_t DecodeSplits(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                            int64_t seq_kv, int64_t cu_count) {
+    const auto& th = kDispatchThresholds;
+    if (batch < 1 || num_kv_heads < 1 || seq_kv < 1) return 1;
+    const int64_t group = num_heads / num_kv_heads;
+    const int64_t heads_per_wg = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    const int64_t wgs_per_split = batch * num_kv_heads * (group / heads_per_wg);
+    const int64_t cus = cu_count > 0 ? cu_count : 256;
+    int64_t splits = (th.workgroups_per_cu * cus + wgs_per_split - 1) / wgs_per_split;
+    const int64_t by_length = (seq_kv + th.min_tokens_per_split - 1) / th.min_tokens_per_split;
+    if (splits > by_length) splits = by_length;
+    if (splits > th.max_splits) splits = th.max_splits;
+    return splits < 1 ? 1 : splits;
+}
+
+}  // namespace detail
+}  // namespace sca
