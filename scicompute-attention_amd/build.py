@@ -112,6 +112,17 @@ def build_host(workers: int) -> str:
     return out
 
 
+def build_cpp_tests() -> str:
+    """The C++ API test program (tests/cpp/test_host_api.cpp), linked against libsca_host.so."""
+    src = os.path.join(REPO_DIR, "tests", "cpp", "test_host_api.cpp")
+    out = os.path.join(LIB_DIR, "test_host_api")
+    tmp = out + ".tmp"
+    _run([CXX, "-std=c++20", "-O1", "-Wall", "-I" + INCLUDE_DIR, src, "-o", tmp, "-L" + LIB_DIR,
+          "-lsca_host", "-lsca_hip", "-Wl,-rpath,$ORIGIN", "-pthread"])
+    os.replace(tmp, out)
+    return out
+
+
 def build(workers: int | None = None) -> list[str]:
     workers = workers or min(8, os.cpu_count() or 4)
     if os.path.isdir(OBJ_DIR):
@@ -119,6 +130,8 @@ def build(workers: int | None = None) -> list[str]:
     outputs = [build_hip(workers)]
     if glob.glob(os.path.join(SRC_DIR, "**", "*.cpp"), recursive=True):
         outputs.append(build_host(workers))
+        if os.path.exists(os.path.join(REPO_DIR, "tests", "cpp", "test_host_api.cpp")):
+            outputs.append(build_cpp_tests())
     return outputs
 
 

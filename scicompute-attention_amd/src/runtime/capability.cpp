@@ -3,6 +3,7 @@
 
 #include <cstdlib>
 #include <mutex>
+#include <string>
 #include <unordered_map>
 
 #include "runtime/internal.hpp"
@@ -28,8 +29,9 @@ DeviceCapability Probe(int device_id) {
         cap.device_name = "gpu-unavailable";
         return cap;
     }
-    cap.device_name = raw.name;
     cap.arch_name = raw.arch_name;
+    // The marketing name can be empty when the driver's name table is not installed.
+    cap.device_name = raw.name[0] != '\0' ? std::string(raw.name) : "AMD " + cap.arch_name;
     cap.major = raw.major;
     cap.minor = raw.minor;
     cap.sm_count = raw.cu_count;
