@@ -195,6 +195,27 @@ def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=16, lo=51
             "mean_len": float(lengths.mean())}
 
 
+# ---- copy calibration ------------------------------------------------------------------------------
+def bench_copy(steps, warmup, mib=256):
+    """A plain copy of known size (the block gather kernel over ids 0..n-1): the reference point
+    that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes, and the practical HBM
+    copy rate."""
+    bs, Hkv, D = 16, 8, 128
+    page = bs * Hkv * D * 2
+    n = mib * (1 << 20) // page
+    src = H.DeviceBuffer(n * page)
+    dst = H.DeviceBuffer(n * page)
+    ids = H.DeviceBuffer.from_array(np.arange(n, dtype=np.int32))
+    shape = H.KvShape()
+    shape.num_blocks, shape.block_size, shape.num_kv_heads, shape.head_dim = n, bs, Hkv, D
+    L = sca_amd.hip_lib()
+    ms = time_launches(lambda: H.check(L.sca_hip_kv_gather(src.ptr, ids.ptr, n, dst.ptr, shape, 2,
+                                                             None)), steps, warmup)
+    nbytes = 2 * n * page
+    return {"ms": ms, "bytes_read": n * page, "bytes_written": n * page,
+            "gbps": nbytes / (ms * 1e-3) / 1e9}
+
+
 # ---- CPU baseline ------------------------------------------------------------------------------------
 def cpu_baseline(max_seconds=12.0):
     import oracle.oracle as orc  # the CPU restatement is the timed baseline
@@ -239,8 +260,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--paged-steps", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "prefill", "paged", "decode"], default="all")
+    ap.add_argument("--only", default="all",
+                    help="comma list of prefill, paged, decode, copy (default: all but copy)")
     args = ap.parse_args()
+    parts = {"prefill", "paged", "decode"} if args.only == "all" else set(args.only.split(","))
+    unknown = parts - {"prefill", "paged", "decode", "copy"}
+    if unknown:
+        ap.error(f"unknown --only part(s): {sorted(unknown)}")
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               f"(this build has no multi-GPU path)", file=sys.stderr)
@@ -251,13 +277,15 @@ def main():
     probe = sca_amd.device_probe(0)
 
     res = {}
-    if args.only in ("all", "prefill"):
+    if "prefill" in parts:
         res["c2_causal"] = bench_flash(args.steps, args.warmup, True)
         res["c2_noncausal"] = bench_flash(args.steps, args.warmup, False)
-    if args.only in ("all", "paged"):
+    if "paged" in parts:
         res["c5_paged"] = bench_paged(args.paged_steps)
-    if args.only in ("all", "decode"):
+    if "decode" in parts:
         res["c4_decode"] = bench_decode(args.steps, args.warmup)
+    if "copy" in parts:
+        res["copy"] = bench_copy(args.steps, args.warmup)
 
     line = {
         "metric": "prefill TFLOP/s (causal S=4096) + paged decode HBM GB/s, 1xMI355X",
@@ -298,6 +326,9 @@ def main():
         line["splitk_decode"] = {"value": round(d["gbps"], 1), "unit": "GB/s", "dtype": "f16",
                                  "ms": round(d["ms"], 4), "splits": d["splits"],
                                  "frac": round(d["gbps"] / PEAK_HBM_GBPS, 4)}
+    if "copy" in res:
+        line["copy_calibration"] = {k: round(v, 4) if isinstance(v, float) else v
+                                    for k, v in res["copy"].items()}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))
