@@ -25,6 +25,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <string>
 
 #include "sca_device.hpp"
@@ -111,6 +112,7 @@ __device__ __forceinline__ uint32_t Half16(const uint4& v, int t) {
 constexpr int kSchedValu = 0x002;
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
+
 
 template <typename E, int D, bool kCausal>
 __global__ __launch_bounds__(FlashGeom<D>::THREADS, 1) void flash_fwd_kernel(
@@ -446,12 +448,23 @@ __global__ __launch_bounds__(FlashGeom<D>::THREADS, 1) void flash_fwd_kernel(
 // ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j % 4 of the 8 bytes
 // read by lane 4*i + j/4 (i = 0..3), i.e. one head-dim column over 4 consecutive keys.
 // ============================================================================================
-template <int D>
+// Two shapes, both 8 waves of 32 query rows x 32 keys per tile:
+//   RG = 4, KQ = 2: 128 query rows, 64-key tiles, a ring of 4 (K, V) stages (non-causal);
+//   RG = 2, KQ = 4: 64 query rows, 128-key tiles, two K slots + two V slots (causal: each
+//   workgroup runs the row tiles t and T-1-t one after the other, so every workgroup gets the
+//   same share of the triangle).
+template <int D, int RG, int KQ>
 struct DmaGeom {
-    static constexpr int BN = 64;                 // keys per tile (2 waves x 32 keys per row group)
-    static constexpr int WAVES = 8;
+    static_assert((RG == 4 && KQ == 2) || (RG == 2 && KQ == 4), "8 waves per workgroup");
+    static constexpr bool kRing4 = RG == 4;
+    static constexpr int BN = 32 * KQ;            // keys per tile (KQ waves x 32 keys per row group)
+    static constexpr int BM = RG * kRowsPerWave;  // query rows per workgroup
+    static constexpr int WAVES = RG * KQ;
     static constexpr int THREADS = WAVES * kWave;
-    static constexpr int STAGES = 4;
+    static constexpr int STAGES = kRing4 ? 4 : 2;
+    // Split layout: K slots (3 when five tiles fit the 160 KB of LDS, so K is fetched two steps
+    // ahead), then two V slots.
+    static constexpr int KSL = kRing4 ? 0 : (5 * BN * D * 2 <= 160 * 1024 ? 3 : 2);
     static constexpr int KS = D / 16;
     static constexpr int DT = D / 32;
     static constexpr int CPR = D / 8;             // 16-byte chunks per row
@@ -460,8 +473,9 @@ struct DmaGeom {
     static constexpr int IPW = BN * CPR / kWave / WAVES;  // DMA instructions per wave per tile
     static constexpr int LOADS_PER_TILE = 2 * IPW;        // K + V, per wave
     static constexpr int MERGE_FLOATS = DT * 16 + 2;
-    static constexpr int MERGE_BYTES = kRowGroups * kWave * MERGE_FLOATS * 4;
-    static constexpr int RING_BYTES = STAGES * STAGE_BYTES;
+    static constexpr int MERGE_BYTES = RG * (KQ - 1) * kWave * MERGE_FLOATS * 4;
+    // kRing4: STAGES stages of (K tile, V tile). Otherwise KSL K tiles then two V tiles.
+    static constexpr int RING_BYTES = kRing4 ? STAGES * STAGE_BYTES : (KSL + 2) * TILE_BYTES;
     static constexpr int LDS_BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
     static_assert(IPW >= 1 && BN * CPR == IPW * kWave * WAVES, "tile must split evenly into DMAs");
 };
@@ -544,15 +558,18 @@ __device__ __forceinline__ void DmaToLds(const uint8_t* base, int num_records, u
                                              voffset, soffset, 0, 0);
 }
 
-template <typename E, int D, bool kCausal>
-__global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
+template <typename E, int D, int RG, int KQ, bool kCausal>
+__global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dma_kernel(
     const sca_flash_params p, int num_q_tiles) {
-    using G = DmaGeom<D>;
+    using G = DmaGeom<D, RG, KQ>;
+    constexpr bool kRing4 = G::kRing4;
     using M = Mfma<E>;
     using vec8 = typename E::vec8;
     constexpr int BN = G::BN;
     constexpr int ROW_BYTES = D * 2;
-    static_assert(2 * G::STAGE_BYTES <= 65536, "stage offsets must fit the 16-bit DS immediate");
+    constexpr int BM = G::BM;
+    static_assert(2 * G::STAGE_BYTES <= 65536 || !kRing4, "stage offsets must fit the 16-bit DS immediate");
+    static_assert(2 * G::TILE_BYTES <= 65536, "slot offsets must fit the 16-bit DS immediate");
 
     extern __shared__ __align__(16) uint8_t lds8[];
     // Stages 0/1 are addressed from lds8, stages 2/3 from lds8 + 2 stages; within each half the
@@ -564,17 +581,21 @@ __global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
     const int lane = tid % kWave;
     const int lr = lane & 31;
     const int hh = lane >> 5;
-    const int rg = wave % kRowGroups;
-    const int kh = wave / kRowGroups;
+    const int rg = wave % RG;
+    const int kh = wave / RG;
 
     const int64_t bh_count = p.batch * p.num_heads;
     const int64_t tile_linear = static_cast<int64_t>(blockIdx.x) / bh_count;
     const int64_t bh = static_cast<int64_t>(blockIdx.x) % bh_count;
-    const int64_t qt = kCausal ? (num_q_tiles - 1 - tile_linear) : tile_linear;
     const int64_t b = bh / p.num_heads;
     const int64_t h = bh % p.num_heads;
     const int64_t h_kv = h / (p.num_heads / p.num_kv_heads);
-    const int q0 = static_cast<int>(qt) * kBlockM;
+    // Causal split-slot workgroups run row tiles t = tile_linear and T-1-t (largest first).
+    constexpr bool kPaired = kCausal && !kRing4;
+    const int passes = kPaired ? ((2 * tile_linear + 1 < num_q_tiles) ? 2 : 1) : 1;
+    // One row tile, start to finish (called once, or twice for a causal pair).
+    auto run_tile = [&](const int64_t qt) __attribute__((always_inline)) {
+    const int q0 = static_cast<int>(qt) * BM;
     const int wave_q0 = q0 + rg * kRowsPerWave;
     const int my_q = wave_q0 + lr;
     const int seq_q = static_cast<int>(p.seq_q);
@@ -604,7 +625,7 @@ __global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
     int n_tiles = (seq_kv + BN - 1) / BN;
     int n_plain = seq_kv / BN;
     if (kCausal) {
-        const int last_key = q0 + kBlockM - 1 + diag;
+        const int last_key = q0 + BM - 1 + diag;
         const int causal_tiles = last_key < 0 ? 0 : last_key / BN + 1;
         if (causal_tiles < n_tiles) n_tiles = causal_tiles;
         const int plain = (q0 + diag + 1) / BN;
@@ -630,6 +651,29 @@ __global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
         dma_voff[i] = row * v_row_bytes + (pos ^ SwzV<D>(row)) * 16;
     }
 
+    // LDS homes of tile t's K and V: RG = 4, stage S = t & 3 holds (K, V); RG = 2, K slot t & 1
+    // and V slot t & 1 (K tiles first, then V tiles).
+    auto v_home = [&]<int S>() -> uint8_t* {
+        return kRing4 ? lds8 + S * G::STAGE_BYTES + G::TILE_BYTES
+                      : lds8 + (G::KSL + S) * G::TILE_BYTES;
+    };
+    // Split layout: K tile t goes to K slot `slot` (= t % KSL, tracked by the caller).
+    auto issue_k = [&](int slot, int t) {
+        uint8_t* k_dst = lds8 + slot * G::TILE_BYTES + wave * G::IPW * 1024;
+        const uint32_t k_tile_off = static_cast<uint32_t>(t * BN * k_row_bytes);
+#pragma unroll
+        for (int i = 0; i < G::IPW; ++i) {
+            DmaToLds(k_bytes, k_records, k_dst + i * 1024, dma_koff[i], k_tile_off);
+        }
+    };
+    auto issue_v = [&]<int S>(int t) {
+        uint8_t* v_dst = v_home.template operator()<S>() + wave * G::IPW * 1024;
+        const uint32_t v_tile_off = static_cast<uint32_t>(t * BN * v_row_bytes);
+#pragma unroll
+        for (int i = 0; i < G::IPW; ++i) {
+            DmaToLds(v_bytes, v_records, v_dst + i * 1024, dma_voff[i], v_tile_off);
+        }
+    };
     auto issue_tile = [&]<int S>(int t) {
         uint8_t* k_dst = lds8 + S * G::STAGE_BYTES + wave * G::IPW * 1024;
         uint8_t* v_dst = k_dst + G::TILE_BYTES;
@@ -674,12 +718,13 @@ __global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
     uint32_t v_frag[G::DT];
 #pragma unroll
     for (int dt = 0; dt < G::DT; ++dt) {
-        v_frag[dt] = G::TILE_BYTES + v_key * ROW_BYTES + (((4 * dt + v_chunk) ^ SwzV<D>(v_key)) * 16) +
-                     v_half;
+        // The V slots of the split layout start 2 tiles in; that base lives in the per-lane
+        // offset so the slot offset stays a DS immediate.
+        v_frag[dt] = (kRing4 ? 0 : G::KSL * G::TILE_BYTES) + v_key * ROW_BYTES +
+                     (((4 * dt + v_chunk) ^ SwzV<D>(v_key)) * 16) + v_half;
     }
 
-    auto qk = [&]<int S>() {
-        const uint8_t* base = (S < 2 ? lds8 : lds_hi) + (S & 1) * G::STAGE_BYTES;
+    auto qk_at = [&](const uint8_t* base) {
         vec8 a[G::KS];
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) a[ks] = *reinterpret_cast<const vec8*>(base + k_frag[ks]);
@@ -690,13 +735,26 @@ __global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
         for (int ks = 0; ks < G::KS; ++ks) acc = M::mma(a[ks], qf[ks], acc);
         return acc;
     };
+    auto qk = [&]<int S>() {
+        return qk_at((S < 2 ? lds8 : lds_hi) + (S & 1) * G::STAGE_BYTES);
+    };
+    auto qk_slot = [&](int slot) { return qk_at(lds8 + slot * G::TILE_BYTES); };
 
     // One pipeline step for tile j (held in stage S; tile j+1 in stage S+1, tiles j+2 and j+3
     // in flight): QK MFMAs of tile j+1 interleaved with the softmax VALU of tile j, the O rescale
     // when some lane's running max moved, PV MFMAs of tile j, then retire tile j+2 and sync.
+    // Split layout (S = j & 1): V of tile j+1 goes to the slot V(j-1) left and K of tile
+    // j+KSL to the slot K(j) left (read by the previous step's QK). V(j+1) and K(j+2) must land
+    // by the end of this step; with three K slots K(j+3) may stay in flight.
     auto step = [&]<bool kMask, int S>(int j, floatx16& s_in, floatx16& s_out) {
-        issue_tile.template operator()<(S + 3) & 3>(j + 3);
-        s_out = qk.template operator()<(S + 1) & 3>();
+        if constexpr (kRing4) {
+            issue_tile.template operator()<(S + 3) & 3>(j + 3);
+            s_out = qk.template operator()<(S + 1) & 3>();
+        } else {
+            issue_v.template operator()<S ^ 1>(j + 1);
+            issue_k(j % G::KSL, j + G::KSL);
+            s_out = qk_slot((j + 1) % G::KSL);
+        }
         floatx16 sv = s_in;
         if constexpr (kMask) {
             const int lim = kCausal ? min(seq_kv - 1, my_q + diag) : seq_kv - 1;
@@ -747,7 +805,9 @@ __global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
 
         const vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
         const vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
-        const uint8_t* vbase = (S < 2 ? lds8 : lds_hi) + (S & 1) * G::STAGE_BYTES;
+        const uint8_t* vbase = kRing4
+                                   ? (S < 2 ? lds8 : lds_hi) + (S & 1) * G::STAGE_BYTES + G::TILE_BYTES
+                                   : lds8 + S * G::TILE_BYTES;
         vec8 va[G::DT][2];
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) {
@@ -763,6 +823,7 @@ __global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
             o[dt] = M::mma(va[dt][0], pb0, o[dt]);
             o[dt] = M::mma(va[dt][1], pb1, o[dt]);
         }
+
         // V^T fragments for two O tiles at a time ahead of their MFMAs
 #pragma unroll
         for (int dt = 0; dt < G::DT; dt += 2) {
@@ -770,47 +831,84 @@ __global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
             __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
         }
 
-        // Tile j+2 has landed (tile j+3 may still be in flight); publish it, and make sure every
-        // wave is done with stage S before it is refilled by the next step.
-        WaitVm<G::LOADS_PER_TILE>();
+        // RG = 4: tile j+2 has landed (tile j+3 may still be in flight). RG = 2: K(j+2) and
+        // V(j+1) have landed. Publish them, and make sure every wave is done with the LDS this
+        // step read before the next step refills it.
+        if constexpr (kRing4) {
+            WaitVm<G::LOADS_PER_TILE>();
+        } else if constexpr (G::KSL == 3) {
+            WaitVm<G::IPW>();
+        } else {
+            WaitVm<0>();
+        }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
     };
 
-    issue_tile.template operator()<0>(0);
-    issue_tile.template operator()<1>(1);
-    issue_tile.template operator()<2>(2);
-    WaitVm<G::LOADS_PER_TILE>();  // tiles 0 and 1 landed (tile 2 may be in flight)
-    __builtin_amdgcn_s_barrier();
-    floatx16 s0 = qk.template operator()<0>();
-    floatx16 s1;
-
+    floatx16 s0, s1;
     int j = 0;
-    // Steady state: four steps per trip, stages fixed at compile time, scores ping-pong s0/s1.
-    for (; j + 4 <= n_plain; j += 4) {
-        step.template operator()<false, 0>(j, s0, s1);
-        step.template operator()<false, 1>(j + 1, s1, s0);
-        step.template operator()<false, 2>(j + 2, s0, s1);
-        step.template operator()<false, 3>(j + 3, s1, s0);
-    }
-    // Remaining plain tiles and the boundary tiles (masking a fully visible tile is harmless).
-    for (; j < n_tiles; ++j) {
-        switch (j & 3) {
-            case 0: step.template operator()<true, 0>(j, s0, s1); break;
-            case 1: step.template operator()<true, 1>(j, s0, s1); break;
-            case 2: step.template operator()<true, 2>(j, s0, s1); break;
-            default: step.template operator()<true, 3>(j, s0, s1); break;
+    if constexpr (kRing4) {
+        issue_tile.template operator()<0>(0);
+        issue_tile.template operator()<1>(1);
+        issue_tile.template operator()<2>(2);
+        WaitVm<G::LOADS_PER_TILE>();  // tiles 0 and 1 landed (tile 2 may be in flight)
+        __builtin_amdgcn_s_barrier();
+        s0 = qk.template operator()<0>();
+        // Steady state: four steps per trip, stages fixed at compile time, scores ping-pong.
+        for (; j + 4 <= n_plain; j += 4) {
+            step.template operator()<false, 0>(j, s0, s1);
+            step.template operator()<false, 1>(j + 1, s1, s0);
+            step.template operator()<false, 2>(j + 2, s0, s1);
+            step.template operator()<false, 3>(j + 3, s1, s0);
         }
-        s0 = s1;
+        // Remaining plain tiles and the boundary tiles (masking a fully visible tile is harmless).
+        for (; j < n_tiles; ++j) {
+            switch (j & 3) {
+                case 0: step.template operator()<true, 0>(j, s0, s1); break;
+                case 1: step.template operator()<true, 1>(j, s0, s1); break;
+                case 2: step.template operator()<true, 2>(j, s0, s1); break;
+                default: step.template operator()<true, 3>(j, s0, s1); break;
+            }
+            s0 = s1;
+        }
+    } else {
+        issue_k(0, 0);
+        issue_k(1, 1);
+        issue_v.template operator()<0>(0);
+        if constexpr (G::KSL == 3) {
+            issue_k(2, 2);
+            WaitVm<G::IPW>();  // K(0), K(1), V(0) landed (K(2) may be in flight)
+        } else {
+            WaitVm<0>();
+        }
+        __builtin_amdgcn_s_barrier();
+        s0 = qk_slot(0);
+        // Every wave has read K(0) before step 0 refills its slot.
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        for (; j + 2 <= n_plain; j += 2) {
+            step.template operator()<false, 0>(j, s0, s1);
+            step.template operator()<false, 1>(j + 1, s1, s0);
+        }
+        for (; j < n_tiles; ++j) {
+            if (j & 1) {
+                step.template operator()<true, 1>(j, s0, s1);
+            } else {
+                step.template operator()<true, 0>(j, s0, s1);
+            }
+            s0 = s1;
+        }
     }
 
     // Drain the trailing DMAs before the LDS is reused for the merge (or released).
     WaitVm<0>();
     __builtin_amdgcn_s_barrier();
 
+    // Merge the KQ key-slices of every row group into the kh == 0 wave.
     {
-        float* mbuf = reinterpret_cast<float*>(lds8) + (rg * kWave + lane) * G::MERGE_FLOATS;
-        if (kh == 1) {
+        float* const merge = reinterpret_cast<float*>(lds8);
+        if (kh != 0) {
+            float* mbuf = merge + (((kh - 1) * RG + rg) * kWave + lane) * G::MERGE_FLOATS;
 #pragma unroll
             for (int dt = 0; dt < G::DT; ++dt) {
 #pragma unroll
@@ -820,20 +918,26 @@ __global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
             mbuf[G::DT * 16 + 1] = l_run;
         }
         __syncthreads();
-        if (kh == 1) return;
-        const float m_o = mbuf[G::DT * 16];
-        const float l_o = mbuf[G::DT * 16 + 1];
-        const float mm = fmaxf(m_used, m_o);
-        const float wa = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
-        const float wb = (m_o == neg_inf()) ? 0.0f : fast_exp2(m_o - mm);
-        m_used = mm;
-        l_run = l_run * wa + l_o * wb;
+        if (kh == 0) {
 #pragma unroll
-        for (int dt = 0; dt < G::DT; ++dt) {
+            for (int q = 1; q < KQ; ++q) {
+                const float* mbuf = merge + (((q - 1) * RG + rg) * kWave + lane) * G::MERGE_FLOATS;
+                const float m_o = mbuf[G::DT * 16];
+                const float l_o = mbuf[G::DT * 16 + 1];
+                const float mm = fmaxf(m_used, m_o);
+                const float wa = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
+                const float wb = (m_o == neg_inf()) ? 0.0f : fast_exp2(m_o - mm);
+                m_used = mm;
+                l_run = l_run * wa + l_o * wb;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[dt][i] = o[dt][i] * wa + mbuf[dt * 16 + i] * wb;
+                for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) o[dt][i] = o[dt][i] * wa + mbuf[dt * 16 + i] * wb;
+                }
+            }
         }
     }
+    if (kh == 0) {
 
     const float l_tot = HalfSum(l_run);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
@@ -855,20 +959,35 @@ __global__ __launch_bounds__(DmaGeom<D>::THREADS, 1) void flash_fwd_dma_kernel(
                 l_tot > 0.0f ? (m_used + __log2f(l_tot)) * kLn2 : neg_inf();
         }
     }
+    }  // kh == 0
+    };  // run_tile
+
+    if constexpr (kPaired) {
+        run_tile(num_q_tiles - 1 - tile_linear);
+        if (passes == 2) {
+            __syncthreads();  // the first tile's merge buffer is the second tile's ring
+            run_tile(tile_linear);
+        }
+    } else {
+        run_tile(kCausal ? num_q_tiles - 1 - tile_linear : tile_linear);
+    }
 }
 
 template <typename E, int D, bool kCausal>
 int LaunchFlash(const sca_flash_params& p, hipStream_t s);
 
-template <typename E, int D, bool kCausal>
+template <typename E, int D, int RG, bool kCausal>
 int LaunchFlashDma(const sca_flash_params& p, hipStream_t s) {
-    using G = DmaGeom<D>;
+    constexpr int KQ = RG == 4 ? 2 : 4;
+    using G = DmaGeom<D, RG, KQ>;
     // Buffer offsets are 32-bit: rows up to seq_kv plus a few tiles of overrun must fit.
     const int64_t extent_k = (p.seq_kv + 4 * G::BN) * p.k_ss * 2;
     const int64_t extent_v = (p.seq_kv + 4 * G::BN) * p.v_ss * 2;
     if (extent_k >= (1LL << 31) || extent_v >= (1LL << 31)) return LaunchFlash<E, D, kCausal>(p, s);
-    const int64_t num_q_tiles = (p.seq_q + kBlockM - 1) / kBlockM;
-    const int64_t blocks = num_q_tiles * p.batch * p.num_heads;
+    const int64_t num_q_tiles = (p.seq_q + G::BM - 1) / G::BM;
+    // Causal split-slot workgroups each take a pair of row tiles.
+    const int64_t row_slots = (kCausal && !G::kRing4) ? (num_q_tiles + 1) / 2 : num_q_tiles;
+    const int64_t blocks = row_slots * p.batch * p.num_heads;
     if (blocks <= 0) return 0;
     if (blocks > 0x7fffffffLL) {
         return SetError(SCA_E_SEQ_TOO_LONG, "flash: grid of " + std::to_string(blocks) +
@@ -877,12 +996,12 @@ int LaunchFlashDma(const sca_flash_params& p, hipStream_t s) {
     static bool attr_set = false;
     if (!attr_set) {
         const hipError_t err = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&flash_fwd_dma_kernel<E, D, kCausal>),
+            reinterpret_cast<const void*>(&flash_fwd_dma_kernel<E, D, RG, KQ, kCausal>),
             hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
         if (err != hipSuccess) (void)hipGetLastError();
         attr_set = true;
     }
-    hipLaunchKernelGGL((flash_fwd_dma_kernel<E, D, kCausal>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((flash_fwd_dma_kernel<E, D, RG, KQ, kCausal>), dim3(static_cast<unsigned>(blocks)),
                        dim3(G::THREADS), G::LDS_BYTES, s, p, static_cast<int>(num_q_tiles));
     return CheckLaunch("flash_fwd_dma_kernel", s);
 }
@@ -912,13 +1031,41 @@ int LaunchFlash(const sca_flash_params& p, hipStream_t s) {
     return CheckLaunch("flash_fwd_kernel", s);
 }
 
+// Row groups of the DMA kernel. Non-causal: 4 (128-row workgroups, the least K/V traffic per
+// FLOP). Causal: 2 (64-row workgroups that each take a complementary pair of row tiles, so every
+// workgroup gets the same share of the triangle) while the 128-row grid would give fewer than two
+// workgroups per CU to balance over, else 4. SCA_FLASH_ROW_GROUPS (2 or 4) overrides the choice,
+// for measurement.
+int DmaRowGroups(const sca_flash_params& p, bool causal) {
+    if (const char* env = std::getenv("SCA_FLASH_ROW_GROUPS")) {
+        const int v = std::atoi(env);
+        if (v == 2 || v == 4) return v;
+    }
+    if (!causal) return 4;
+    static int cu_count = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        return n > 0 ? n : 256;
+    }();
+    const int64_t tiles128 = (p.seq_q + 127) / 128 * p.batch * p.num_heads;
+    return tiles128 < 2 * static_cast<int64_t>(cu_count) ? 2 : 4;
+}
+
 template <typename E, bool kCausal>
 int LaunchForDim(const sca_flash_params& p, hipStream_t s) {
     switch (p.head_dim) {
         case 32: return LaunchFlash<E, 32, kCausal>(p, s);
-        case 64: return LaunchFlashDma<E, 64, kCausal>(p, s);
+        case 64:
+            return DmaRowGroups(p, kCausal) == 2 ? LaunchFlashDma<E, 64, 2, kCausal>(p, s)
+                                                 : LaunchFlashDma<E, 64, 4, kCausal>(p, s);
         case 96: return LaunchFlash<E, 96, kCausal>(p, s);
-        case 128: return LaunchFlashDma<E, 128, kCausal>(p, s);
+        case 128:
+            return DmaRowGroups(p, kCausal) == 2 ? LaunchFlashDma<E, 128, 2, kCausal>(p, s)
+                                                 : LaunchFlashDma<E, 128, 4, kCausal>(p, s);
         case 160: return LaunchFlash<E, 160, kCausal>(p, s);
         case 192: return LaunchFlash<E, 192, kCausal>(p, s);
         case 256: return LaunchFlash<E, 256, kCausal>(p, s);
@@ -933,9 +1080,9 @@ bool Aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 int LdsBytesFor(int64_t head_dim) {
     switch (head_dim) {
         case 32: return FlashGeom<32>::LDS_BYTES;
-        case 64: return DmaGeom<64>::LDS_BYTES;
+        case 64: return DmaGeom<64, 4, 2>::LDS_BYTES;
         case 96: return FlashGeom<96>::LDS_BYTES;
-        case 128: return DmaGeom<128>::LDS_BYTES;
+        case 128: return DmaGeom<128, 4, 2>::LDS_BYTES;
         case 160: return FlashGeom<160>::LDS_BYTES;
         case 192: return FlashGeom<192>::LDS_BYTES;
         case 256: return FlashGeom<256>::LDS_BYTES;
@@ -978,9 +1125,9 @@ int sca_hip_flash_tile(int32_t head_dim, int32_t* block_m, int32_t* block_n, int
         default: break;
     }
     if (dma) {
-        bn = sca_hip::DmaGeom<64>::BN;
-        nw = sca_hip::DmaGeom<64>::WAVES;
-        ns = sca_hip::DmaGeom<64>::STAGES;
+        bn = sca_hip::DmaGeom<64, 4, 2>::BN;
+        nw = sca_hip::DmaGeom<64, 4, 2>::WAVES;
+        ns = sca_hip::DmaGeom<64, 4, 2>::STAGES;
     }
     if (block_m != nullptr) *block_m = sca_hip::kBlockM;
     if (block_n != nullptr) *block_n = bn;

@@ -8,7 +8,8 @@ import os
 import numpy as np
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
-LIB_DIR = os.path.join(PKG_ROOT, "lib")
+# SCA_LIB_DIR points the bindings at another build of the same libraries (measurement only).
+LIB_DIR = os.environ.get("SCA_LIB_DIR") or os.path.join(PKG_ROOT, "lib")
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 COPY_H2D, COPY_D2H, COPY_D2D = 1, 2, 3
