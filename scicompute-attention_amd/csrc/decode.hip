@@ -398,37 +398,45 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_partial_kernel(const sc
     }
 }
 
-// One wave per (b, h_q): merges the splits (reference decode_splitk.cu:143-182).
+// Split merge (reference decode_splitk.cu:143-182): out = sum_s O_s e^{m_s - m*} / sum_s l_s e^{m_s - m*},
+// with m* = max_s m_s, splits with m_s = -inf skipped and out = 0 when the denominator is 0.
+// One thread per (b, h_q, 4 consecutive d): the split loads of a thread are independent, so
+// they overlap instead of forming a chain, and neighbouring threads read neighbouring bytes.
+constexpr int kCombineThreads = 256;
+
 template <typename E, int D>
-__global__ __launch_bounds__(256) void decode_combine_kernel(const sca_decode_params p) {
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const sca_decode_params p) {
     constexpr int64_t kElemBytes = 16 / E::VE;
-    const int lane = threadIdx.x % kWave;
-    const int64_t flat_bh = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) +
-                            threadIdx.x / kWave;
+    constexpr int kQuads = D / 4;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kCombineThreads + threadIdx.x;
+    const int64_t flat_bh = idx / kQuads;
     if (flat_bh >= p.batch * p.num_heads) return;
+    const int d0 = static_cast<int>(idx % kQuads) * 4;
     const int64_t b = flat_bh / p.num_heads;
     const int64_t h = flat_bh % p.num_heads;
-    const int64_t base = flat_bh * p.num_splits;
+    const int ns = static_cast<int>(p.num_splits);
+    const float* pm = p.partial_m + flat_bh * ns;
+    const float* pl = p.partial_l + flat_bh * ns;
+    const float* po = p.partial_o + flat_bh * ns * D + d0;
 
     float m_all = neg_inf();
-    for (int64_t s = 0; s < p.num_splits; ++s) m_all = fmaxf(m_all, p.partial_m[base + s]);
+#pragma unroll 8
+    for (int s = 0; s < ns; ++s) m_all = fmaxf(m_all, pm[s]);
     float l_all = 0.0f;
-    for (int64_t s = 0; s < p.num_splits; ++s) {
-        const float ms = p.partial_m[base + s];
-        if (ms == neg_inf()) continue;
-        l_all += p.partial_l[base + s] * fast_exp2((ms - m_all) * kLog2e);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+    for (int s = 0; s < ns; ++s) {
+        const float ms = pm[s];
+        const float w = (ms == neg_inf()) ? 0.0f : fast_exp2((ms - m_all) * kLog2e);
+        l_all = fmaf(pl[s], w, l_all);
+        const float* o = po + static_cast<int64_t>(s) * D;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(o[i], w, acc[i]);
     }
     const float inv = l_all > 0.0f ? 1.0f / l_all : 0.0f;
     uint8_t* out_row = static_cast<uint8_t*>(p.out) + (b * p.o_sb + h * p.o_sh) * kElemBytes;
-    for (int d = lane; d < D; d += kWave) {
-        float total = 0.0f;
-        for (int64_t s = 0; s < p.num_splits; ++s) {
-            const float ms = p.partial_m[base + s];
-            if (ms == neg_inf()) continue;
-            total += p.partial_o[(base + s) * D + d] * fast_exp2((ms - m_all) * kLog2e);
-        }
-        E::store1(out_row, d, total * inv);
-    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) E::store1(out_row, d0 + i, acc[i] * inv);
 }
 
 template <typename E, int D, int kHeads, bool kPaged>
@@ -455,9 +463,9 @@ int LaunchForDim(const sca_decode_params& p, hipStream_t s) {
         rc = LaunchPartial<E, D, 1, kPaged>(p, static_cast<int>(group), s);
     }
     if (rc != 0 || p.num_splits == 1) return rc;
-    const int64_t waves = p.batch * p.num_heads;
-    const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
-    hipLaunchKernelGGL((decode_combine_kernel<E, D>), dim3(blocks), dim3(256), 0, s, p);
+    const int64_t threads = p.batch * p.num_heads * (D / 4);
+    const unsigned blocks = static_cast<unsigned>((threads + kCombineThreads - 1) / kCombineThreads);
+    hipLaunchKernelGGL((decode_combine_kernel<E, D>), dim3(blocks), dim3(kCombineThreads), 0, s, p);
     return CheckLaunch("decode_combine_kernel", s);
 }
 
