@@ -22,7 +22,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <string>
+#include <type_traits>
 
 #include "sca_device.hpp"
 
@@ -439,6 +441,360 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const s
     for (int i = 0; i < 4; ++i) E::store1(out_row, d0 + i, acc[i] * inv);
 }
 
+// ---- MFMA partial kernel (fp16/bf16, head_dim 64 or 128, power-of-two pages) -----------------
+// One workgroup per (b, kv head, 16-head chunk of its q group, split); four waves take the
+// 32-token tiles of the split in turn and are merged through LDS at the end.
+//   S^T[32 tokens x 16 heads] = K . Q^T on v_mfma_f32_16x16x32 (two 16-token row tiles; the
+//     q heads of the group fill the 16 columns, unused columns hold zero queries);
+//   O^T[D x 16 heads] += V^T . P^T, one MFMA per 16 dims with the 32 tokens as the k dimension.
+// Lane layout: lane l owns query head l % 16; its S^T values are tokens 16r + 4(l/16) + i.
+// The PV k index 8g + i (g = l/16) maps to token 4g + i for i < 4 and 16 + 4g + (i - 4) after,
+// which is exactly the register order of the two S^T tiles, so P^T needs no data movement.
+// The head dimension is permuted identically for K and Q: k step j, lane group g covers
+// elements (4j + g)*8 .. +8, so K goes straight from global memory into the A-operand
+// registers as 64-byte row blocks. V goes global -> LDS with global_load_lds_dwordx4 into a
+// two-stage ring per wave (one LDS object per stage, so the compiler's LDS-DMA tracking waits
+// only for the stage being read); V rows XOR their 32-byte segments so the transposed reads
+// hit distinct banks. A wave always has the next tile in flight while it computes, and the
+// 64 KB ring lets two workgroups share a CU.
+constexpr int kMfmaTile = 32;   // tokens per wave iteration
+constexpr int kMfmaHeads = 16;  // query heads per workgroup (MFMA N)
+
+template <typename E>
+struct DecMfma;
+
+template <>
+struct DecMfma<DecF16> {
+    using vec8 = half8;
+    using Tr = TrRead<F16>;
+    typedef _Float16 pair_t __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ floatx4 mma(const vec8& a, const vec8& b, floatx4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack(float a, float b) {
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, pair_t));
+    }
+};
+
+template <>
+struct DecMfma<DecBF16> {
+    using vec8 = bf16x8;
+    using Tr = TrRead<BF16>;
+    typedef __bf16 pair_t __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ floatx4 mma(const vec8& a, const vec8& b, floatx4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack(float a, float b) {
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, pair_t));
+    }
+};
+
+template <int D>
+struct MfmaDecGeom {
+    static_assert(D == 64 || D == 128, "MFMA decode covers head_dim 64 and 128");
+    static constexpr int NK = D / 32;                    // QK k steps
+    static constexpr int ND = D / 16;                    // PV output tiles
+    static constexpr int RB = 2 * D;                     // row bytes
+    static constexpr int CPR = D / 8;                    // 16-byte chunks per row
+    static constexpr int TILE_BYTES = kMfmaTile * RB;    // one V tile of one wave
+    static constexpr int DMA = TILE_BYTES / 1024;        // DMA instructions per V tile
+    static constexpr int ROWS_PER_DMA = 64 / CPR;
+    static constexpr int SLOT_BYTES = kDecodeWaves * TILE_BYTES;  // one LDS object
+    static constexpr int LOADS = DMA + 2 * NK;           // vector memory instructions per tile
+    static_assert(kDecodeWaves * kMfmaHeads * D * 4 <= SLOT_BYTES, "merge buffer fits one slot");
+};
+
+// 32-byte segment swizzle of V row t (rows t and t + 16 share it, which the two transposed
+// reads of a lane rely on).
+template <int D>
+__device__ __forceinline__ int VSwz(int t) {
+    return D == 128 ? (t & 7) : ((t >> 1) & 3);
+}
+
+template <typename E, int D, bool kPaged>
+__global__ __launch_bounds__(kDecodeThreads) void decode_mfma_kernel(const sca_decode_params p,
+                                                                     int h_chunks,
+                                                                     int block_shift) {
+    using G = MfmaDecGeom<D>;
+    using M = DecMfma<E>;
+    using vec8 = typename M::vec8;
+
+    __shared__ __align__(16) uint8_t s_v0[G::SLOT_BYTES];
+    __shared__ __align__(16) uint8_t s_v1[G::SLOT_BYTES];
+    __shared__ int32_t s_pages[kPaged ? kPageSegment : 1];
+    __shared__ float s_m[kDecodeWaves][kMfmaHeads];
+    __shared__ float s_l[kDecodeWaves][kMfmaHeads];
+
+    const int lane = threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int col = lane % 16;  // query head within the chunk; row/column index of the MFMA
+    const int grp = lane / 16;  // lane group
+
+    const int64_t split = blockIdx.x;
+    const int64_t h_kv = blockIdx.y / h_chunks;
+    const int64_t h_chunk = blockIdx.y % h_chunks;
+    const int64_t b = blockIdx.z;
+    const int64_t group = p.num_heads / p.num_kv_heads;
+    const int64_t h0 = h_kv * group + h_chunk * kMfmaHeads;
+    const int hc = static_cast<int>(group - h_chunk * kMfmaHeads < kMfmaHeads
+                                        ? group - h_chunk * kMfmaHeads
+                                        : kMfmaHeads);
+    const float scale2 = p.scale * kLog2e;
+    const int64_t bs_mask = (int64_t{1} << block_shift) - 1;
+
+    // Q^T B operand: lane (col, grp) holds head col, elements (4j + grp)*8 .. +8 for k step j.
+    vec8 qb[G::NK];
+    {
+        const uint8_t* q_row =
+            static_cast<const uint8_t*>(p.q) + (b * p.q_sb + (h0 + col) * p.q_sh) * 2;
+#pragma unroll
+        for (int j = 0; j < G::NK; ++j) {
+            const uint4 raw = col < hc ? *reinterpret_cast<const uint4*>(q_row + (4 * j + grp) * 16)
+                                       : make_uint4(0, 0, 0, 0);
+            qb[j] = __builtin_bit_cast(vec8, raw);
+        }
+    }
+
+    floatx4 o[G::ND];
+#pragma unroll
+    for (int dt = 0; dt < G::ND; ++dt) o[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = neg_inf();  // running max of head `col` (log2 units, identical across lane groups)
+    float l = 0.0f;       // this lane's share of the running denominator
+
+    const int64_t len = p.seq_lens != nullptr ? static_cast<int64_t>(p.seq_lens[b]) : p.seq_kv;
+    const int64_t chunk = len > 0 ? (len + p.num_splits - 1) / p.num_splits : 0;
+    const int64_t t_begin = split * chunk;
+    const int64_t t_end = (t_begin + chunk < len) ? (t_begin + chunk) : len;
+
+    const uint8_t* k_base =
+        static_cast<const uint8_t*>(p.k) + ((kPaged ? 0 : b * p.k_sb) + h_kv * p.k_sh) * 2;
+    const uint8_t* v_base =
+        static_cast<const uint8_t*>(p.v) + ((kPaged ? 0 : b * p.v_sb) + h_kv * p.v_sh) * 2;
+    const int64_t k_row_bytes = p.k_ss * 2;
+    const int64_t v_row_bytes = p.v_ss * 2;
+
+    // Per-lane constants: DMA row/chunk within one instruction and the V transposed read
+    // (row 4*grp + col/4, byte 8*(col%4) of a 32-byte segment).
+    const int dma_row = lane / G::CPR;
+    const int dma_pc = lane % G::CPR;
+    const int wave_off = wave * G::TILE_BYTES;
+    const int tr_row = 4 * grp + col / 4;
+    const int tr_rd = wave_off + tr_row * G::RB + 8 * (col % 4);
+    const int tr_x = VSwz<D>(tr_row) * 32;
+
+    const int64_t seg_tokens = kPaged ? (static_cast<int64_t>(kPageSegment) << block_shift)
+                                      : (t_end - t_begin);
+    for (int64_t seg = t_begin; seg < t_end; seg += (seg_tokens > 0 ? seg_tokens : 1)) {
+        const int64_t seg_end = (seg + seg_tokens < t_end) ? seg + seg_tokens : t_end;
+        int64_t page0 = 0;
+        if constexpr (kPaged) {
+            page0 = seg >> block_shift;
+            const int64_t n_pages = ((seg_end - 1) >> block_shift) - page0 + 1;
+            __syncthreads();
+            for (int64_t i = threadIdx.x; i < n_pages; i += kDecodeThreads) {
+                const int64_t logical = page0 + i;
+                int32_t id = -1;
+                if (logical < p.max_blocks_per_seq) {
+                    id = p.page_table[b * p.max_blocks_per_seq + logical];
+                    if (id < 0 || id >= p.num_kv_blocks) id = -1;
+                }
+                s_pages[i] = id;
+            }
+            __syncthreads();
+        }
+        // Row index of token tok (< 0: the token contributes nothing); branch-free.
+        auto row_of = [&](int64_t tok) -> int64_t {
+            const bool in = tok < seg_end;
+            if constexpr (kPaged) {
+                const int rel = static_cast<int>((in ? tok : seg) - (page0 << block_shift));
+                const int32_t id = s_pages[rel >> block_shift];
+                const int64_t r = (static_cast<int64_t>(id) << block_shift) | (rel & bs_mask);
+                return (in && id >= 0) ? r : -1;
+            } else {
+                return in ? tok : -1;
+            }
+        };
+        // Masked tokens read a row that is always mapped (row 0 of the pool, or the segment's
+        // first token); their scores are set to -inf and their V rows cleared before use.
+        const int64_t safe_row = kPaged ? 0 : seg;
+
+        const int n_tiles = static_cast<int>((seg_end - seg + kMfmaTile - 1) / kMfmaTile);
+        // V tile -> LDS stage, then the K tile -> registers (row col of each row tile).
+        auto issue = [&](int tile, uint8_t* vdst, uint4 (&kr)[2][G::NK]) {
+            const int64_t base = seg + static_cast<int64_t>(tile) * kMfmaTile;
+#pragma unroll
+            for (int i = 0; i < G::DMA; ++i) {
+                const int t = i * G::ROWS_PER_DMA + dma_row;
+                int64_t r = row_of(base + t);
+                r = r < 0 ? safe_row : r;
+                const int vc = (((dma_pc >> 1) ^ VSwz<D>(t)) << 1) | (dma_pc & 1);
+                __builtin_amdgcn_global_load_lds(
+                    v_base + r * v_row_bytes + vc * 16,
+                    (__attribute__((address_space(3))) void*)(vdst + wave_off + i * 1024), 16, 0, 0);
+            }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                int64_t r = row_of(base + 16 * rt + col);
+                r = r < 0 ? safe_row : r;
+                const uint8_t* src = k_base + r * k_row_bytes + grp * 16;
+#pragma unroll
+                for (int j = 0; j < G::NK; ++j) kr[rt][j] = *reinterpret_cast<const uint4*>(src + j * 64);
+            }
+        };
+        auto compute = [&](int tile, const uint4 (&kr)[2][G::NK], uint8_t* vs) {
+            const int64_t base = seg + static_cast<int64_t>(tile) * kMfmaTile;
+            // Token validity of the tile: bit t for token t.
+            const uint64_t b0 = __builtin_amdgcn_ballot_w64(row_of(base + col) >= 0);
+            const uint64_t b1 = __builtin_amdgcn_ballot_w64(row_of(base + 16 + col) >= 0);
+            const uint32_t valid_mask = static_cast<uint32_t>(b0 & 0xffffu) |
+                                        (static_cast<uint32_t>(b1 & 0xffffu) << 16);
+            // S^T = K . Q^T for the two 16-token row tiles.
+            floatx4 s[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                s[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < G::NK; ++j) {
+                    s[rt] = M::mma(__builtin_bit_cast(vec8, kr[rt][j]), qb[j], s[rt]);
+                }
+            }
+            float sv[2][4];
+            float mx = neg_inf();
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * rt + 4 * grp + i;
+                    const float x = ((valid_mask >> t) & 1u) ? s[rt][i] * scale2 : neg_inf();
+                    sv[rt][i] = x;
+                    mx = fmaxf(mx, x);
+                }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_new = fmaxf(m, mx);
+            if (__builtin_amdgcn_ballot_w64(m_new > m) != 0) {
+                const float alpha = (m == neg_inf()) ? 0.0f : fast_exp2(m - m_new);
+                l *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < G::ND; ++dt) o[dt] *= alpha;
+                m = m_new;
+            }
+            const float m_use = (m == neg_inf()) ? 0.0f : m;
+            float pr[2][4];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pr[rt][i] = fast_exp2(sv[rt][i] - m_use);
+                    l += pr[rt][i];
+                }
+            }
+            const vec8 pb = __builtin_bit_cast(
+                vec8, make_uint4(M::pack(pr[0][0], pr[0][1]), M::pack(pr[0][2], pr[0][3]),
+                                 M::pack(pr[1][0], pr[1][1]), M::pack(pr[1][2], pr[1][3])));
+            if (valid_mask != 0xffffffffu) {
+                // Clear the V rows of masked tokens: their probabilities are zero, but the rows
+                // may hold any bit pattern.
+                constexpr int kLanesPerRow = kWave / kMfmaTile;
+                constexpr int kChunksPerLane = G::CPR / kLanesPerRow;
+                const int t = lane / kLanesPerRow;
+                if (((valid_mask >> t) & 1u) == 0) {
+                    uint4* rowp = reinterpret_cast<uint4*>(vs + wave_off + t * G::RB) +
+                                  (lane % kLanesPerRow) * kChunksPerLane;
+#pragma unroll
+                    for (int c = 0; c < kChunksPerLane; ++c) rowp[c] = make_uint4(0, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int dt = 0; dt < G::ND; ++dt) {
+                const uint8_t* a = vs + tr_rd + ((dt * 32) ^ tr_x);
+                const uint2 lo = M::Tr::read(a);
+                const uint2 hi = M::Tr::read(a + 16 * G::RB);
+                o[dt] = M::mma(__builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y)), pb,
+                               o[dt]);
+            }
+        };
+
+        // Tiles wave, wave + 4, ...: stage 0 holds the even ones of this wave, stage 1 the odd.
+        uint4 k0[2][G::NK], k1[2][G::NK];
+        int tile = wave;
+        if (tile < n_tiles) issue(tile, s_v0, k0);
+        if (tile + kDecodeWaves < n_tiles) issue(tile + kDecodeWaves, s_v1, k1);
+        while (tile < n_tiles) {
+            if (tile + kDecodeWaves < n_tiles) {
+                WaitVm<G::LOADS>();
+            } else {
+                WaitVm<0>();
+            }
+            compute(tile, k0, s_v0);
+            if (tile + 2 * kDecodeWaves < n_tiles) issue(tile + 2 * kDecodeWaves, s_v0, k0);
+            tile += kDecodeWaves;
+            if (tile >= n_tiles) break;
+            if (tile + kDecodeWaves < n_tiles) {
+                WaitVm<G::LOADS>();
+            } else {
+                WaitVm<0>();
+            }
+            compute(tile, k1, s_v1);
+            if (tile + 2 * kDecodeWaves < n_tiles) issue(tile + 2 * kDecodeWaves, s_v1, k1);
+            tile += kDecodeWaves;
+        }
+    }
+
+    // Lane totals of l over the four lane groups; wave states to LDS.
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    __syncthreads();  // every wave is done with its stages
+    float* s_o = reinterpret_cast<float*>(s_v0);  // [wave][head][D]
+#pragma unroll
+    for (int dt = 0; dt < G::ND; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s_o[(wave * kMfmaHeads + col) * D + dt * 16 + 4 * grp + i] = o[dt][i];
+        }
+    }
+    if (grp == 0) {
+        s_m[wave][col] = m;
+        s_l[wave][col] = l;
+    }
+    __syncthreads();
+
+    const bool direct = p.num_splits == 1;
+    for (int idx = threadIdx.x; idx < hc * D; idx += kDecodeThreads) {
+        const int h = idx / D;
+        const int d = idx % D;
+        float mm = neg_inf();
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) mm = fmaxf(mm, s_m[w][h]);
+        float lsum = 0.0f, osum = 0.0f;
+        if (mm != neg_inf()) {
+#pragma unroll
+            for (int w = 0; w < kDecodeWaves; ++w) {
+                const float mw = s_m[w][h];
+                const float wgt = mw == neg_inf() ? 0.0f : fast_exp2(mw - mm);
+                lsum += s_l[w][h] * wgt;
+                osum += s_o[(w * kMfmaHeads + h) * D + d] * wgt;
+            }
+        }
+        const int64_t hq = h0 + h;
+        if (direct) {
+            const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+            uint8_t* out_row = static_cast<uint8_t*>(p.out) + (b * p.o_sb + hq * p.o_sh) * 2;
+            E::store1(out_row, d, osum * inv);
+        } else {
+            const int64_t flat = (b * p.num_heads + hq) * p.num_splits + split;
+            p.partial_o[flat * D + d] = osum;
+            if (d == 0) {
+                p.partial_m[flat] = (mm == neg_inf()) ? neg_inf() : mm * kLn2;
+                p.partial_l[flat] = lsum;
+            }
+        }
+    }
+}
+
 template <typename E, int D, int kHeads, bool kPaged>
 int LaunchPartial(const sca_decode_params& p, int h_chunks, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(p.num_splits),
@@ -449,11 +805,39 @@ int LaunchPartial(const sca_decode_params& p, int h_chunks, hipStream_t s) {
     return CheckLaunch("decode_partial_kernel", s);
 }
 
+// SCA_DECODE_MFMA=0 selects the VALU kernels for every shape (measurement and comparison).
+bool MfmaDecodeEnabled() {
+    static const bool enabled = [] {
+        const char* v = std::getenv("SCA_DECODE_MFMA");
+        return v == nullptr || v[0] != '0';
+    }();
+    return enabled;
+}
+
 template <typename E, int D, bool kPaged>
 int LaunchForDim(const sca_decode_params& p, hipStream_t s) {
     const int64_t group = p.num_heads / p.num_kv_heads;
     int rc = 0;
-    if (group % 8 == 0) {
+    int block_shift = 0;
+    if constexpr (kPaged) {
+        while ((int64_t{1} << block_shift) < p.block_size) ++block_shift;
+    }
+    const bool mfma_ok = !std::is_same_v<E, DecF32> && (D == 64 || D == 128) &&
+                         (!kPaged || (int64_t{1} << block_shift) == p.block_size) &&
+                         MfmaDecodeEnabled();
+    if constexpr (!std::is_same_v<E, DecF32> && (D == 64 || D == 128)) {
+        if (mfma_ok) {
+            const int h_chunks = static_cast<int>((group + kMfmaHeads - 1) / kMfmaHeads);
+            const dim3 grid(static_cast<unsigned>(p.num_splits),
+                            static_cast<unsigned>(p.num_kv_heads * h_chunks),
+                            static_cast<unsigned>(p.batch));
+            hipLaunchKernelGGL((decode_mfma_kernel<E, D, kPaged>), grid, dim3(kDecodeThreads), 0, s,
+                               p, h_chunks, block_shift);
+            rc = CheckLaunch("decode_mfma_kernel", s);
+        }
+    }
+    if (mfma_ok) {
+    } else if (group % 8 == 0) {
         rc = LaunchPartial<E, D, 8, kPaged>(p, static_cast<int>(group / 8), s);
     } else if (group % 4 == 0) {
         rc = LaunchPartial<E, D, 4, kPaged>(p, static_cast<int>(group / 4), s);

@@ -516,36 +516,6 @@ __device__ __forceinline__ float HalfSum(float v) {
     return lo + hi;
 }
 
-template <typename E>
-struct TrRead;
-
-template <>
-struct TrRead<F16> {
-    typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 v4;
-    static __device__ __forceinline__ uint2 read(const uint8_t* lds_byte_ptr) {
-        const v4 r = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-            (__attribute__((address_space(3))) v4*)(lds_byte_ptr));
-        return __builtin_bit_cast(uint2, r);
-    }
-};
-
-template <>
-struct TrRead<BF16> {
-    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 v4;
-    static __device__ __forceinline__ uint2 read(const uint8_t* lds_byte_ptr) {
-        const v4 r = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (__attribute__((address_space(3))) v4*)(lds_byte_ptr));
-        return __builtin_bit_cast(uint2, r);
-    }
-};
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt bits [3:0] and [15:14]).
-template <int N>
-__device__ __forceinline__ void WaitVm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
-
 // 16-byte DMA of lane data from a raw buffer (base, num_records) at voffset + soffset into LDS
 // at lds + 16 * lane. Bytes at or beyond num_records read as zero. (The buffer resource is
 // built here rather than in the kernel body: a buffer-resource local in a kernel body makes the

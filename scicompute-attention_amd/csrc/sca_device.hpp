@@ -72,6 +72,38 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
+// Transposed LDS read (ds_read_b64_tr_b16): within each 16-lane group, lane j receives element
+// j % 4 of the 8 bytes addressed by lane 4*i + j/4, i = 0..3 (one column over four rows).
+template <typename E>
+struct TrRead;
+
+template <>
+struct TrRead<F16> {
+    typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 v4;
+    static __device__ __forceinline__ uint2 read(const uint8_t* lds_byte_ptr) {
+        const v4 r = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (__attribute__((address_space(3))) v4*)(lds_byte_ptr));
+        return __builtin_bit_cast(uint2, r);
+    }
+};
+
+template <>
+struct TrRead<BF16> {
+    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 v4;
+    static __device__ __forceinline__ uint2 read(const uint8_t* lds_byte_ptr) {
+        const v4 r = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (__attribute__((address_space(3))) v4*)(lds_byte_ptr));
+        return __builtin_bit_cast(uint2, r);
+    }
+};
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt bits [3:0] and [15:14]).
+template <int N>
+__device__ __forceinline__ void WaitVm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
 }  // namespace sca_hip
 
 // Error reporting of the C ABI (defined in runtime.hip).

@@ -118,3 +118,10 @@ def test_rejects_bad_arguments(hip):
     with pytest.raises(H.HipError) as exc:
         H.decode_splitk(p)
     assert exc.value.code == 2001
+
+
+def test_groups_wider_than_one_mfma_tile(hip):
+    # 16 query heads share one MFMA tile: group 32 takes two chunks, group 24 a partial second
+    _case("f16", 2, 32, 1, 700, 128, 3, 77001)
+    _case("bf16", 1, 24, 1, 515, 64, 2, 77002)
+    _case("bf16", 2, 16, 1, 95, 128, 1, 77003)

@@ -131,3 +131,30 @@ def test_null_seq_lens_uses_pool_upper_bound(hip):
     full = 3 * bs  # 3 mapped pages
     ref = reference(qd, kd, vd, table, [full], bs, nb)
     check_attention(out.reshape(-1, D), ref, "f16", "paged null seq_lens")
+
+
+@pytest.mark.parametrize("bs,D", [(1, 64), (16, 128), (32, 64)])
+def test_nan_outside_attended_rows_is_never_used(hip, bs, D):
+    # Every pool row that no sequence attends (free blocks, the tail of each last page) holds
+    # NaN bits: tiles that straddle a sequence's end or an unmapped page must not let them in.
+    lengths = [37, 1, 100, 16 * 5 + 3]
+    Hq, Hkv = 8, 2
+    nb, mb, table, kb, kd, vb, vd = build_pool(lengths, bs, Hkv, D, "bf16", 85001 + bs)
+    table[2, 1] = -1
+    used = np.zeros((nb, bs), bool)
+    for s, L in enumerate(lengths):
+        for t in range(L):
+            page = table[s, t // bs]
+            if 0 <= page < nb:
+                used[page, t % bs] = True
+    kb = kb.copy()
+    vb = vb.copy()
+    kb[~used] = 0x7FC0
+    vb[~used] = 0x7FC0
+    q = uniform((len(lengths), Hq, 1, D), 85001)
+    qb, qd = quantize(q, "bf16")
+    for splits in (1, 3):
+        out = run_paged(qb, kb, vb, table, lengths, "bf16", Hq=Hq, Hkv=Hkv, D=D, bs=bs,
+                        num_blocks=nb, splits=splits)
+        ref = reference(qd, kd, vd, table, lengths, bs, nb)
+        check_attention(out.reshape(-1, D), ref, "bf16", f"paged NaN pool bs={bs} D={D}")
