@@ -61,6 +61,13 @@ def bf16_bits(rng, shape, chunk=1 << 24):
     return bits.reshape(shape)
 
 
+def dispatcher_splits(batch, Hq, Hkv, seq_kv, D):
+    """The split count the host dispatcher picks for this decode shape on this device."""
+    from sca_amd import host as SH
+    cus = H.device_probe(0).cu_count
+    return SH.decode_splits(SH.AttentionShape(batch, 1, seq_kv, Hq, Hkv, D), cus)
+
+
 def time_launches(launch, steps, warmup):
     for _ in range(warmup):
         launch()
@@ -100,7 +107,9 @@ def bench_flash(steps, warmup, causal, B=1, Hh=8, S=4096, D=128):
 
 
 # ---- C4: split-K decode --------------------------------------------------------------------------
-def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=8):
+def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=None):
+    if splits is None:
+        splits = dispatcher_splits(B, Hq, Hkv, S, D)
     rng = np.random.default_rng(4004)
     dq = H.DeviceBuffer.from_array(f16_bits(rng, (B, Hq, 1, D)))
     dk = H.DeviceBuffer.from_array(f16_bits(rng, (B, Hkv, S, D)))
@@ -124,7 +133,7 @@ def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=8):
 
 
 # ---- C5: paged decode ------------------------------------------------------------------------------
-def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=16, lo=512, hi=16384):
+def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=512, hi=16384):
     rng = np.random.default_rng(5005)
     lengths = rng.integers(lo, hi + 1, size=num_seqs).astype(np.int64)
     final = lengths + steps
@@ -132,6 +141,8 @@ def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=16, lo=51
     num_blocks = int(need.sum()) + 64
     perm = rng.permutation(num_blocks).astype(np.int32)
     max_blocks = int(need.max())
+    if splits is None:  # the paged path sizes splits from the pool, as the host layer does
+        splits = dispatcher_splits(num_seqs, Hq, Hkv, num_blocks * bs, D)
     table = np.full((num_seqs, max_blocks), -1, np.int32)
     pos = 0
     for s in range(num_seqs):
@@ -166,6 +177,8 @@ def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=16, lo=51
     p.dtype = H.DTYPE_BF16
     p.page_table, p.block_size, p.max_blocks_per_seq = dt.ptr, bs, max_blocks
     p.num_kv_blocks, p.seq_lens = num_blocks, dlens.ptr
+    dorder = H.DeviceBuffer(num_seqs * 8)
+    p.batch_order = dorder.ptr
     L = sca_amd.hip_lib()
     cur = lengths.copy()
     total_ms, total_bytes = 0.0, 0

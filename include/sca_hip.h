@@ -184,6 +184,10 @@ typedef struct sca_decode_params {
     int64_t max_blocks_per_seq;
     int64_t num_kv_blocks;
     const int32_t* seq_lens; /* optional per-sequence lengths (device), else seq_kv for all */
+    /* optional device scratch of 2*batch int32 (8-byte aligned); with seq_lens set, the
+     * sequences are scheduled longest first through it (no reference counterpart: the reference
+     * launches sequences in batch order). NULL = batch order. */
+    int32_t* batch_order;
 } sca_decode_params;
 
 /* FP32 scratch elements the partials need: batch*num_heads*num_splits*(2 + head_dim). */

@@ -513,7 +513,10 @@ __device__ __forceinline__ int VSwz(int t) {
     return D == 128 ? (t & 7) : ((t >> 1) & 3);
 }
 
-template <typename E, int D, bool kPaged>
+// kWaveHeads: each wave owns one (kv head, head chunk) slot and all tiles of the split (the
+// four waves read neighbouring head slices of the same token rows); otherwise the four waves
+// share the tiles of one head slot and are merged through LDS.
+template <typename E, int D, bool kPaged, bool kWaveHeads>
 __global__ __launch_bounds__(kDecodeThreads) void decode_mfma_kernel(const sca_decode_params p,
                                                                      int h_chunks,
                                                                      int block_shift) {
@@ -533,9 +536,22 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_mfma_kernel(const sca_d
     const int grp = lane / 16;  // lane group
 
     const int64_t split = blockIdx.x;
-    const int64_t h_kv = blockIdx.y / h_chunks;
-    const int64_t h_chunk = blockIdx.y % h_chunks;
-    const int64_t b = blockIdx.z;
+    const int64_t slots = p.num_kv_heads * h_chunks;
+    const int64_t hh = kWaveHeads ? static_cast<int64_t>(blockIdx.y) * kDecodeWaves + wave
+                                  : static_cast<int64_t>(blockIdx.y);
+    const bool slot_ok = hh < slots;  // false only for trailing waves of a kWaveHeads grid
+    const int64_t h_kv = (slot_ok ? hh : 0) / h_chunks;
+    const int64_t h_chunk = (slot_ok ? hh : 0) % h_chunks;
+    // Sequence of this workgroup: batch order, or longest first through batch_order.
+    int64_t b = blockIdx.z;
+    int64_t len = p.seq_kv;
+    if (p.batch_order != nullptr) {
+        const int2 e = reinterpret_cast<const int2*>(p.batch_order)[blockIdx.z];
+        b = e.x;
+        len = e.y;
+    } else if (p.seq_lens != nullptr) {
+        len = p.seq_lens[b];
+    }
     const int64_t group = p.num_heads / p.num_kv_heads;
     const int64_t h0 = h_kv * group + h_chunk * kMfmaHeads;
     const int hc = static_cast<int>(group - h_chunk * kMfmaHeads < kMfmaHeads
@@ -563,7 +579,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_mfma_kernel(const sca_d
     float m = neg_inf();  // running max of head `col` (log2 units, identical across lane groups)
     float l = 0.0f;       // this lane's share of the running denominator
 
-    const int64_t len = p.seq_lens != nullptr ? static_cast<int64_t>(p.seq_lens[b]) : p.seq_kv;
     const int64_t chunk = len > 0 ? (len + p.num_splits - 1) / p.num_splits : 0;
     const int64_t t_begin = split * chunk;
     const int64_t t_end = (t_begin + chunk < len) ? (t_begin + chunk) : len;
@@ -620,7 +635,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_mfma_kernel(const sca_d
         // first token); their scores are set to -inf and their V rows cleared before use.
         const int64_t safe_row = kPaged ? 0 : seg;
 
-        const int n_tiles = static_cast<int>((seg_end - seg + kMfmaTile - 1) / kMfmaTile);
+        const int n_tiles =
+            slot_ok ? static_cast<int>((seg_end - seg + kMfmaTile - 1) / kMfmaTile) : 0;
+        constexpr int TS = kWaveHeads ? 1 : kDecodeWaves;  // tile stride of one wave
         // V tile -> LDS stage, then the K tile -> registers (row col of each row tile).
         auto issue = [&](int tile, uint8_t* vdst, uint4 (&kr)[2][G::NK]) {
             const int64_t base = seg + static_cast<int64_t>(tile) * kMfmaTile;
@@ -720,33 +737,61 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_mfma_kernel(const sca_d
 
         // Tiles wave, wave + 4, ...: stage 0 holds the even ones of this wave, stage 1 the odd.
         uint4 k0[2][G::NK], k1[2][G::NK];
-        int tile = wave;
+        int tile = kWaveHeads ? 0 : wave;
         if (tile < n_tiles) issue(tile, s_v0, k0);
-        if (tile + kDecodeWaves < n_tiles) issue(tile + kDecodeWaves, s_v1, k1);
+        if (tile + TS < n_tiles) issue(tile + TS, s_v1, k1);
         while (tile < n_tiles) {
-            if (tile + kDecodeWaves < n_tiles) {
+            if (tile + TS < n_tiles) {
                 WaitVm<G::LOADS>();
             } else {
                 WaitVm<0>();
             }
             compute(tile, k0, s_v0);
-            if (tile + 2 * kDecodeWaves < n_tiles) issue(tile + 2 * kDecodeWaves, s_v0, k0);
-            tile += kDecodeWaves;
+            if (tile + 2 * TS < n_tiles) issue(tile + 2 * TS, s_v0, k0);
+            tile += TS;
             if (tile >= n_tiles) break;
-            if (tile + kDecodeWaves < n_tiles) {
+            if (tile + TS < n_tiles) {
                 WaitVm<G::LOADS>();
             } else {
                 WaitVm<0>();
             }
             compute(tile, k1, s_v1);
-            if (tile + 2 * kDecodeWaves < n_tiles) issue(tile + 2 * kDecodeWaves, s_v1, k1);
-            tile += kDecodeWaves;
+            if (tile + 2 * TS < n_tiles) issue(tile + 2 * TS, s_v1, k1);
+            tile += TS;
         }
     }
 
-    // Lane totals of l over the four lane groups; wave states to LDS.
+    // Lane totals of l over the four lane groups.
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
+    const bool direct = p.num_splits == 1;
+    if constexpr (kWaveHeads) {
+        // This wave holds the whole state of its head slot: lane (col, grp) has dims
+        // dt*16 + 4*grp + i of head h0 + col.
+        if (!slot_ok || col >= hc) return;
+        const int64_t hq = h0 + col;
+        if (direct) {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            uint8_t* out_row = static_cast<uint8_t*>(p.out) + (b * p.o_sb + hq * p.o_sh) * 2;
+#pragma unroll
+            for (int dt = 0; dt < G::ND; ++dt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) E::store1(out_row, dt * 16 + 4 * grp + i, o[dt][i] * inv);
+            }
+        } else {
+            const int64_t flat = (b * p.num_heads + hq) * p.num_splits + split;
+#pragma unroll
+            for (int dt = 0; dt < G::ND; ++dt) {
+                *reinterpret_cast<floatx4*>(p.partial_o + flat * D + dt * 16 + 4 * grp) = o[dt];
+            }
+            if (grp == 0) {
+                p.partial_m[flat] = (m == neg_inf()) ? neg_inf() : m * kLn2;
+                p.partial_l[flat] = l;
+            }
+        }
+        return;
+    }
+    // Wave states to LDS, then one thread per (head, dim) merges the four waves.
     __syncthreads();  // every wave is done with its stages
     float* s_o = reinterpret_cast<float*>(s_v0);  // [wave][head][D]
 #pragma unroll
@@ -762,7 +807,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_mfma_kernel(const sca_d
     }
     __syncthreads();
 
-    const bool direct = p.num_splits == 1;
     for (int idx = threadIdx.x; idx < hc * D; idx += kDecodeThreads) {
         const int h = idx / D;
         const int d = idx % D;
@@ -805,6 +849,25 @@ int LaunchPartial(const sca_decode_params& p, int h_chunks, hipStream_t s) {
     return CheckLaunch("decode_partial_kernel", s);
 }
 
+// Longest-first schedule of ragged sequences: entry r of `order` is (b, len_b) for the sequence
+// of rank r (descending length, ties by index). The MFMA kernels take the sequence of grid
+// row z from entry z, so the longest sequences are dispatched first.
+constexpr int kMaxOrderedBatch = 8192;
+
+__global__ __launch_bounds__(256) void decode_order_kernel(const int32_t* seq_lens, int batch,
+                                                           int32_t* order) {
+    const int b = blockIdx.x * 256 + threadIdx.x;
+    if (b >= batch) return;
+    const int mine = seq_lens[b];
+    int rank = 0;
+    for (int j = 0; j < batch; ++j) {
+        const int other = seq_lens[j];
+        rank += (other > mine) | ((other == mine) & (j < b));
+    }
+    order[2 * rank] = b;
+    order[2 * rank + 1] = mine;
+}
+
 // SCA_DECODE_MFMA=0 selects the VALU kernels for every shape (measurement and comparison).
 bool MfmaDecodeEnabled() {
     static const bool enabled = [] {
@@ -812,6 +875,15 @@ bool MfmaDecodeEnabled() {
         return v == nullptr || v[0] != '0';
     }();
     return enabled;
+}
+
+// Head slot per wave (SCA_DECODE_WAVE_HEADS=1/0 forces it on/off; default: paged only).
+bool MfmaWaveHeads(bool paged) {
+    static const int mode = [] {
+        const char* v = std::getenv("SCA_DECODE_WAVE_HEADS");
+        return v == nullptr ? -1 : (v[0] == '0' ? 0 : 1);
+    }();
+    return mode < 0 ? paged : mode == 1;
 }
 
 template <typename E, int D, bool kPaged>
@@ -827,12 +899,29 @@ int LaunchForDim(const sca_decode_params& p, hipStream_t s) {
                          MfmaDecodeEnabled();
     if constexpr (!std::is_same_v<E, DecF32> && (D == 64 || D == 128)) {
         if (mfma_ok) {
+            sca_decode_params q = p;
+            if (q.seq_lens == nullptr || q.batch > kMaxOrderedBatch) q.batch_order = nullptr;
+            if (q.batch_order != nullptr) {
+                hipLaunchKernelGGL(decode_order_kernel,
+                                   dim3(static_cast<unsigned>((q.batch + 255) / 256)), dim3(256),
+                                   0, s, q.seq_lens, static_cast<int>(q.batch), q.batch_order);
+                rc = CheckLaunch("decode_order_kernel", s);
+                if (rc != 0) return rc;
+            }
             const int h_chunks = static_cast<int>((group + kMfmaHeads - 1) / kMfmaHeads);
-            const dim3 grid(static_cast<unsigned>(p.num_splits),
-                            static_cast<unsigned>(p.num_kv_heads * h_chunks),
-                            static_cast<unsigned>(p.batch));
-            hipLaunchKernelGGL((decode_mfma_kernel<E, D, kPaged>), grid, dim3(kDecodeThreads), 0, s,
-                               p, h_chunks, block_shift);
+            const int64_t slots = p.num_kv_heads * h_chunks;
+            if (MfmaWaveHeads(kPaged)) {
+                const dim3 grid(static_cast<unsigned>(p.num_splits),
+                                static_cast<unsigned>((slots + kDecodeWaves - 1) / kDecodeWaves),
+                                static_cast<unsigned>(p.batch));
+                hipLaunchKernelGGL((decode_mfma_kernel<E, D, kPaged, true>), grid,
+                                   dim3(kDecodeThreads), 0, s, q, h_chunks, block_shift);
+            } else {
+                const dim3 grid(static_cast<unsigned>(p.num_splits), static_cast<unsigned>(slots),
+                                static_cast<unsigned>(p.batch));
+                hipLaunchKernelGGL((decode_mfma_kernel<E, D, kPaged, false>), grid,
+                                   dim3(kDecodeThreads), 0, s, q, h_chunks, block_shift);
+            }
             rc = CheckLaunch("decode_mfma_kernel", s);
         }
     }
@@ -906,6 +995,9 @@ int ValidateDecode(const sca_decode_params* p, bool paged) {
         p->v_sb % ve || p->v_sh % ve || p->v_ss % ve || p->o_sb % ve || p->o_sh % ve) {
         return SetError(SCA_E_LAYOUT_MISMATCH,
                         "decode: pointers must be 16 B aligned and strides multiples of 16 B");
+    }
+    if ((reinterpret_cast<uintptr_t>(p->batch_order) & 7u) != 0) {
+        return SetError(SCA_E_LAYOUT_MISMATCH, "decode: batch_order must be 8 B aligned");
     }
     if (paged) {
         if (p->page_table == nullptr) {

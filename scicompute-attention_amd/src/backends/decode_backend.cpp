@@ -33,21 +33,30 @@ int64_t ResolveSplits(int64_t requested, int64_t batch, int64_t num_heads, int64
 }
 
 // Points the partial pointers of `p` into the pooled FP32 scratch (m | l | O).
+// Binds the FP32 partials (splits > 1) and, for ragged lengths, the 2*batch int32 schedule the
+// kernels sort the sequences into, both from the decode scratch buffer.
 sci::Status BindPartials(sca_decode_params* p, int64_t splits, int device_id, size_t* bytes) {
-    const int64_t elements = PartialElements(p->batch, p->num_heads, splits, p->head_dim);
-    *bytes = static_cast<size_t>(elements) * sizeof(float);
-    if (splits == 1) {  // the kernel writes the output directly
-        p->partial_m = p->partial_l = p->partial_o = nullptr;
-        *bytes = 0;
-        return sci::Status::Ok();
-    }
+    const int64_t partials =
+        splits == 1 ? 0 : PartialElements(p->batch, p->num_heads, splits, p->head_dim);
+    const int64_t order = p->seq_lens != nullptr ? 2 * p->batch : 0;
+    const int64_t elements = partials + order;
+    *bytes = static_cast<size_t>(partials) * sizeof(float);
+    p->partial_m = p->partial_l = p->partial_o = nullptr;
+    p->batch_order = nullptr;
+    if (elements == 0) return sci::Status::Ok();  // splits == 1 writes the output directly
     sci::Result<float*> scratch = runtime::AcquireScratchFp32(
         runtime::ScratchKind::kDecodePartials, static_cast<size_t>(elements), device_id);
     if (!scratch.ok()) return scratch.error();
-    const int64_t base = p->batch * p->num_heads * splits;
-    p->partial_m = *scratch;
-    p->partial_l = *scratch + base;
-    p->partial_o = *scratch + 2 * base;
+    if (partials > 0) {
+        const int64_t base = p->batch * p->num_heads * splits;
+        p->partial_m = *scratch;
+        p->partial_l = *scratch + base;
+        p->partial_o = *scratch + 2 * base;
+    }
+    if (order > 0) {
+        // partials is even (base * (2 + head_dim) with an even head_dim): 8-byte aligned.
+        p->batch_order = reinterpret_cast<int32_t*>(*scratch + partials);
+    }
     return sci::Status::Ok();
 }
 

@@ -26,22 +26,23 @@ inline constexpr DispatchThresholds kDispatchThresholds{
     /* decode_max_seq_q     */ 1,
     /* decode_min_seq_kv    */ 256,
     /* short_max_seq_kv     */ 128,
-    /* min_tokens_per_split */ 256,
-    /* workgroups_per_cu    */ 4,
+    /* min_tokens_per_split */ 512,
+    /* workgroups_per_cu    */ 6,
     /* max_splits           */ 64,
     /* revision             */ "r0-mi355x",
 };
 
-// Split count of the decode kernels for `batch` sequences of up to `seq_kv` keys. The kernel runs
-// one workgroup per (sequence, KV head, split) and serves the whole GQA group of a KV head when
-// the group size is a multiple of 8, 4 or 2 (smaller groups need several workgroups per KV head).
+// Split count of the decode kernels for `batch` sequences of up to `seq_kv` keys. The MFMA
+// kernel runs one workgroup per (sequence, split, four KV-head slots), a slot being one KV head
+// and up to 16 of its query heads; splits are added until every CU holds `workgroups_per_cu`
+// workgroups, while each split keeps at least `min_tokens_per_split` keys.
 inline int64_t DecodeSplits(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
                             int64_t seq_kv, int64_t cu_count) {
     const auto& th = kDispatchThresholds;
     if (batch < 1 || num_kv_heads < 1 || seq_kv < 1) return 1;
     const int64_t group = num_heads / num_kv_heads;
-    const int64_t heads_per_wg = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
-    const int64_t wgs_per_split = batch * num_kv_heads * (group / heads_per_wg);
+    const int64_t slots = num_kv_heads * ((group + 15) / 16);
+    const int64_t wgs_per_split = batch * ((slots + 3) / 4);
     const int64_t cus = cu_count > 0 ? cu_count : 256;
     int64_t splits = (th.workgroups_per_cu * cus + wgs_per_split - 1) / wgs_per_split;
     const int64_t by_length = (seq_kv + th.min_tokens_per_split - 1) / th.min_tokens_per_split;

@@ -40,7 +40,7 @@ def build_pool(lengths, bs, Hkv, D, dtype, seed, slack=3, gen="uniform"):
 
 
 def run_paged(qb, kb, vb, table, lengths, dtype, *, Hq, Hkv, D, bs, num_blocks, splits,
-              pass_lens=True):
+              pass_lens=True, longest_first=True):
     S = len(lengths)
     max_blocks = table.shape[1]
     dq = H.DeviceBuffer.from_array(qb)
@@ -57,6 +57,8 @@ def run_paged(qb, kb, vb, table, lengths, dtype, *, Hq, Hkv, D, bs, num_blocks, 
     p.max_blocks_per_seq = max_blocks
     p.num_kv_blocks = num_blocks
     p.seq_lens = dl.ptr if pass_lens else None
+    order = H.DeviceBuffer(8 * S)
+    p.batch_order = order.ptr if longest_first else None
     H.decode_splitk_paged(p)
     sca_amd.synchronize()
     return to_float(dout.download(np.uint16), dtype).reshape(S, Hq, D)
@@ -73,15 +75,16 @@ def reference(qd, kd, vd, table, lengths, bs, num_blocks):
     return np.concatenate(outs)
 
 
-def _case(lengths, bs, Hq, Hkv, D, dtype, seed, splits=16, gen="uniform"):
+def _case(lengths, bs, Hq, Hkv, D, dtype, seed, splits=16, gen="uniform", longest_first=True):
     nb, mb, table, kb, kd, vb, vd = build_pool(lengths, bs, Hkv, D, dtype, seed, gen=gen)
     q = uniform((len(lengths), Hq, 1, D), seed) if gen == "uniform" else \
         normal((len(lengths), Hq, 1, D), seed)
     qb, qd = quantize(q, dtype)
     out = run_paged(qb, kb, vb, table, lengths, dtype, Hq=Hq, Hkv=Hkv, D=D, bs=bs, num_blocks=nb,
-                    splits=splits)
+                    splits=splits, longest_first=longest_first)
     ref = reference(qd, kd, vd, table, lengths, bs, nb)
-    tag = f"paged {dtype} lens={lengths[:4]} bs={bs} Hq={Hq} Hkv={Hkv} D={D} splits={splits}"
+    tag = (f"paged {dtype} lens={lengths[:4]} bs={bs} Hq={Hq} Hkv={Hkv} D={D} splits={splits} "
+           f"longest_first={longest_first}")
     print(tag, flush=True)
     check_attention(out.reshape(-1, D), ref, dtype, tag)
 
@@ -102,6 +105,8 @@ def test_many_ragged_sequences_bf16(hip):
     lengths = rng.integers(1, 3000, size=12).tolist()
     _case(lengths, 16, 32, 8, 128, "bf16", 82001, gen="normal")
     _case(lengths, 16, 32, 8, 128, "bf16", 82002, splits=1, gen="normal")
+    _case(lengths, 16, 32, 8, 128, "bf16", 82003, splits=3, gen="normal", longest_first=False)
+    _case(lengths + [0, 5], 16, 32, 8, 64, "f16", 82004, splits=4)
 
 
 def test_unmapped_pages_contribute_nothing(hip):
