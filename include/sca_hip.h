@@ -184,9 +184,10 @@ typedef struct sca_decode_params {
     int64_t max_blocks_per_seq;
     int64_t num_kv_blocks;
     const int32_t* seq_lens; /* optional per-sequence lengths (device), else seq_kv for all */
-    /* optional device scratch of 2*batch int32 (8-byte aligned); with seq_lens set, the
-     * sequences are scheduled longest first through it (no reference counterpart: the reference
-     * launches sequences in batch order). NULL = batch order. */
+    /* optional device scratch of 2*batch int32 (8-byte aligned). With seq_lens set, sequences
+     * are scheduled longest first; batches of up to 256 sequences are ranked inside the kernel,
+     * larger ones (up to 8192) through this scratch (no reference counterpart: the reference
+     * launches sequences in batch order). NULL = batch order above 256 sequences. */
     int32_t* batch_order;
 } sca_decode_params;
 

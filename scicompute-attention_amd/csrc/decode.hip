@@ -441,6 +441,8 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const s
     for (int i = 0; i < 4; ++i) E::store1(out_row, d0 + i, acc[i] * inv);
 }
 
+constexpr int kRankBatch = 256;  // ragged batches up to this size are ranked in the kernel
+
 // ---- MFMA partial kernel (fp16/bf16, head_dim 64 or 128, power-of-two pages) -----------------
 // One workgroup per (b, kv head, 16-head chunk of its q group, split); four waves take the
 // 32-token tiles of the split in turn and are merged through LDS at the end.
@@ -526,7 +528,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_mfma_kernel(const sca_d
 
     __shared__ __align__(16) uint8_t s_v0[G::SLOT_BYTES];
     __shared__ __align__(16) uint8_t s_v1[G::SLOT_BYTES];
-    __shared__ int32_t s_pages[kPaged ? kPageSegment : 1];
+    // Page ids of the current segment; first the lengths of a ragged batch being ranked.
+    __shared__ int32_t s_pages[kPaged ? kPageSegment : kRankBatch];
+    __shared__ int32_t s_seq[2];
     __shared__ float s_m[kDecodeWaves][kMfmaHeads];
     __shared__ float s_l[kDecodeWaves][kMfmaHeads];
 
@@ -542,10 +546,32 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_mfma_kernel(const sca_d
     const bool slot_ok = hh < slots;  // false only for trailing waves of a kWaveHeads grid
     const int64_t h_kv = (slot_ok ? hh : 0) / h_chunks;
     const int64_t h_chunk = (slot_ok ? hh : 0) % h_chunks;
-    // Sequence of this workgroup: batch order, or longest first through batch_order.
+    // Sequence of this workgroup. Ragged batches run longest first: grid row z takes the
+    // sequence of rank z (descending length, ties by index), ranked here for batches of up to
+    // kRankBatch sequences and by decode_order_kernel through batch_order above that.
     int64_t b = blockIdx.z;
     int64_t len = p.seq_kv;
-    if (p.batch_order != nullptr) {
+    if (p.seq_lens != nullptr && p.batch <= kRankBatch) {
+        const int tid = threadIdx.x;
+        const int nb = static_cast<int>(p.batch);
+        if (tid < nb) s_pages[tid] = p.seq_lens[tid];
+        __syncthreads();
+        if (tid < nb) {
+            const int mine = s_pages[tid];
+            int rank = 0;
+            for (int j = 0; j < nb; ++j) {
+                const int other = s_pages[j];
+                rank += (other > mine) | ((other == mine) & (j < tid));
+            }
+            if (rank == static_cast<int>(blockIdx.z)) {
+                s_seq[0] = tid;
+                s_seq[1] = mine;
+            }
+        }
+        __syncthreads();
+        b = __builtin_amdgcn_readfirstlane(s_seq[0]);
+        len = __builtin_amdgcn_readfirstlane(s_seq[1]);
+    } else if (p.batch_order != nullptr) {
         const int2 e = reinterpret_cast<const int2*>(p.batch_order)[blockIdx.z];
         b = e.x;
         len = e.y;
@@ -849,9 +875,9 @@ int LaunchPartial(const sca_decode_params& p, int h_chunks, hipStream_t s) {
     return CheckLaunch("decode_partial_kernel", s);
 }
 
-// Longest-first schedule of ragged sequences: entry r of `order` is (b, len_b) for the sequence
-// of rank r (descending length, ties by index). The MFMA kernels take the sequence of grid
-// row z from entry z, so the longest sequences are dispatched first.
+// Longest-first schedule of ragged batches larger than kRankBatch: entry r of `order` is
+// (b, len_b) for the sequence of rank r (descending length, ties by index). The MFMA kernels
+// take the sequence of grid row z from entry z, so the longest sequences are dispatched first.
 constexpr int kMaxOrderedBatch = 8192;
 
 __global__ __launch_bounds__(256) void decode_order_kernel(const int32_t* seq_lens, int batch,
@@ -900,7 +926,9 @@ int LaunchForDim(const sca_decode_params& p, hipStream_t s) {
     if constexpr (!std::is_same_v<E, DecF32> && (D == 64 || D == 128)) {
         if (mfma_ok) {
             sca_decode_params q = p;
-            if (q.seq_lens == nullptr || q.batch > kMaxOrderedBatch) q.batch_order = nullptr;
+            if (q.seq_lens == nullptr || q.batch <= kRankBatch || q.batch > kMaxOrderedBatch) {
+                q.batch_order = nullptr;
+            }
             if (q.batch_order != nullptr) {
                 hipLaunchKernelGGL(decode_order_kernel,
                                    dim3(static_cast<unsigned>((q.batch + 255) / 256)), dim3(256),

@@ -163,3 +163,11 @@ def test_nan_outside_attended_rows_is_never_used(hip, bs, D):
                         num_blocks=nb, splits=splits)
         ref = reference(qd, kd, vd, table, lengths, bs, nb)
         check_attention(out.reshape(-1, D), ref, "bf16", f"paged NaN pool bs={bs} D={D}")
+
+
+def test_large_ragged_batch_ranked_through_scratch(hip):
+    # more than 256 sequences: the longest-first order comes from the batch_order scratch
+    rng = np.random.default_rng(86001)
+    lengths = rng.integers(0, 90, size=300).tolist()
+    _case(lengths, 16, 8, 2, 64, "f16", 86001, splits=2)
+    _case(lengths, 16, 8, 2, 64, "f16", 86002, splits=3, longest_first=False)
