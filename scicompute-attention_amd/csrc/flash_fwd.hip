@@ -589,7 +589,8 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
             if (my_q < seq_q) raw = *reinterpret_cast<const uint4*>(q_row + 16 * ks);
             qf[ks] = __builtin_bit_cast(vec8, raw);
         }
-        WaitVm<0>();  // Q is in registers before any tile DMA is counted
+        // No wait here: the Q loads are older than every tile DMA, so each vmcnt wait below
+        // that retires a tile also retires them, and the first QK waits for them by itself.
     }
 
     int n_tiles = (seq_kv + BN - 1) / BN;
@@ -716,7 +717,9 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     // Split layout (S = j & 1): V of tile j+1 goes to the slot V(j-1) left and K of tile
     // j+KSL to the slot K(j) left (read by the previous step's QK). V(j+1) and K(j+2) must land
     // by the end of this step; with three K slots K(j+3) may stay in flight.
-    auto step = [&]<bool kMask, int S>(int j, floatx16& s_in, floatx16& s_out) {
+    // kMaskable && masked: the tile reaches past the causal diagonal or the end of the keys
+    // (`masked` is uniform; kMaskable = false compiles the plain step).
+    auto step = [&]<bool kMaskable, int S>(int j, floatx16& s_in, floatx16& s_out, bool masked) {
         if constexpr (kRing4) {
             issue_tile.template operator()<(S + 3) & 3>(j + 3);
             s_out = qk.template operator()<(S + 1) & 3>();
@@ -726,7 +729,7 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
             s_out = qk_slot((j + 1) % G::KSL);
         }
         floatx16 sv = s_in;
-        if constexpr (kMask) {
+        if (kMaskable && masked) {
             const int lim = kCausal ? min(seq_kv - 1, my_q + diag) : seq_kv - 1;
             const int kbase = j * BN + wkey_base + 4 * hh;
 #pragma unroll
@@ -826,18 +829,18 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
         s0 = qk.template operator()<0>();
         // Steady state: four steps per trip, stages fixed at compile time, scores ping-pong.
         for (; j + 4 <= n_plain; j += 4) {
-            step.template operator()<false, 0>(j, s0, s1);
-            step.template operator()<false, 1>(j + 1, s1, s0);
-            step.template operator()<false, 2>(j + 2, s0, s1);
-            step.template operator()<false, 3>(j + 3, s1, s0);
+            step.template operator()<false, 0>(j, s0, s1, false);
+            step.template operator()<false, 1>(j + 1, s1, s0, false);
+            step.template operator()<false, 2>(j + 2, s0, s1, false);
+            step.template operator()<false, 3>(j + 3, s1, s0, false);
         }
         // Remaining plain tiles and the boundary tiles (masking a fully visible tile is harmless).
         for (; j < n_tiles; ++j) {
             switch (j & 3) {
-                case 0: step.template operator()<true, 0>(j, s0, s1); break;
-                case 1: step.template operator()<true, 1>(j, s0, s1); break;
-                case 2: step.template operator()<true, 2>(j, s0, s1); break;
-                default: step.template operator()<true, 3>(j, s0, s1); break;
+                case 0: step.template operator()<true, 0>(j, s0, s1, true); break;
+                case 1: step.template operator()<true, 1>(j, s0, s1, true); break;
+                case 2: step.template operator()<true, 2>(j, s0, s1, true); break;
+                default: step.template operator()<true, 3>(j, s0, s1, true); break;
             }
             s0 = s1;
         }
@@ -856,18 +859,13 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
         // Every wave has read K(0) before step 0 refills its slot.
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
-        for (; j + 2 <= n_plain; j += 2) {
-            step.template operator()<false, 0>(j, s0, s1);
-            step.template operator()<false, 1>(j + 1, s1, s0);
+        // Two steps per trip (stages fixed at compile time); tiles from n_plain on are masked
+        // through a uniform flag, so the boundary tiles stay in the same code path.
+        for (; j + 2 <= n_tiles; j += 2) {
+            step.template operator()<true, 0>(j, s0, s1, j >= n_plain);
+            step.template operator()<true, 1>(j + 1, s1, s0, j + 1 >= n_plain);
         }
-        for (; j < n_tiles; ++j) {
-            if (j & 1) {
-                step.template operator()<true, 1>(j, s0, s1);
-            } else {
-                step.template operator()<true, 0>(j, s0, s1);
-            }
-            s0 = s1;
-        }
+        if (j < n_tiles) step.template operator()<true, 0>(j, s0, s1, j >= n_plain);
     }
 
     // Drain the trailing DMAs before the LDS is reused for the merge (or released).
