@@ -208,6 +208,66 @@ def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=
             "mean_len": float(lengths.mean())}
 
 
+# ---- C5 through the host layer (PagedKVCache + sca::paged_attention) ------------------------------
+def bench_paged_host(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, lo=512, hi=16384):
+    """C5 as a serving loop drives it: the pool is filled through PagedKVCache::AppendTokens with
+    the page-sized appends of all sequences in a seeded random order (so every sequence's pages
+    are scattered over the pool), then each step appends one token to every sequence with one
+    AppendTokensBatch, syncs the page table (changed entries only) and calls
+    sca::paged_attention. The attend call is timed with HIP events around the API call
+    (dispatcher and allocation included); append + sync are timed the same way, separately."""
+    from sca_amd import host as SH
+    rng = np.random.default_rng(5006)
+    lengths = rng.integers(lo, hi + 1, size=num_seqs).astype(np.int64)
+    num_blocks = int(((lengths + steps + bs - 1) // bs).sum()) + 64
+    cache = SH.PagedKVCache(SH.KVCacheConfig(1, Hkv, D, bs, num_blocks, num_seqs, "bf16"))
+    chunk = SH.Tensor.from_numpy(bf16_bits(rng, (bs, Hkv, D)), "bf16")
+    order = np.concatenate([np.full((L + bs - 1) // bs, s) for s, L in enumerate(lengths)])
+    rng.shuffle(order)
+    filled = np.zeros(num_seqs, np.int64)
+    tails = {}
+    for s in order:
+        n = int(min(bs, lengths[s] - filled[s]))
+        if n == bs:
+            cache.append_tokens(int(s), 0, chunk, chunk)
+        else:
+            t = tails.setdefault(n, SH.Tensor.from_numpy(bf16_bits(rng, (n, Hkv, D)), "bf16"))
+            cache.append_tokens(int(s), 0, t, t)
+        filled[s] += n
+    q = SH.Tensor.from_numpy(bf16_bits(rng, (num_seqs, Hq, 1, D)), "bf16")
+    tok = SH.Tensor.from_numpy(bf16_bits(rng, (num_seqs, Hkv, D)), "bf16")
+    lens_dev = H.DeviceBuffer(num_seqs * 4)
+    ids = np.arange(num_seqs)
+    start, mid, stop = H.Event(), H.Event(), H.Event()
+    cur = lengths.copy()
+    t_attend = t_append = 0.0
+    total_bytes = 0
+    splits = None
+    for step in range(steps + 2):  # two untimed warmup steps
+        timed = step >= 2
+        start.record()
+        cache.append_batch(ids, 0, tok, tok)
+        cache.sync_page_table()
+        cur = cur + 1
+        lens_dev.upload(cur.astype(np.int32))
+        mid.record()
+        res = SH.paged_attention(q, cache, {"seq_lens": lens_dev.ptr, "num_seqs": num_seqs,
+                                            "block_size": bs})
+        stop.record()
+        stop.synchronize()
+        splits = res.stats.get("num_splits")
+        del res
+        if timed:
+            t_append += start.elapsed_ms(mid)
+            t_attend += mid.elapsed_ms(stop)
+            total_bytes += int(cur.sum()) * Hkv * D * 2 * 2 + \
+                int(((cur + bs - 1) // bs).sum()) * 4 + 2 * num_seqs * Hq * D * 2
+    ms = t_attend / steps
+    nbytes = total_bytes / steps
+    return {"ms": ms, "gbps": nbytes / (ms * 1e-3) / 1e9, "append_sync_ms": t_append / steps,
+            "splits": splits, "num_blocks": num_blocks}
+
+
 # ---- copy calibration ------------------------------------------------------------------------------
 def bench_copy(steps, warmup, mib=256):
     """A plain copy of known size (the block gather kernel over ids 0..n-1): the reference point
@@ -274,10 +334,12 @@ def main():
     ap.add_argument("--paged-steps", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="all",
-                    help="comma list of prefill, paged, decode, copy (default: all but copy)")
+                    help="comma list of prefill, paged, paged_host, decode, copy "
+                         "(default: all but copy)")
     args = ap.parse_args()
-    parts = {"prefill", "paged", "decode"} if args.only == "all" else set(args.only.split(","))
-    unknown = parts - {"prefill", "paged", "decode", "copy"}
+    parts = ({"prefill", "paged", "paged_host", "decode"} if args.only == "all"
+             else set(args.only.split(",")))
+    unknown = parts - {"prefill", "paged", "paged_host", "decode", "copy"}
     if unknown:
         ap.error(f"unknown --only part(s): {sorted(unknown)}")
     if args.gpus != 1:
@@ -295,6 +357,8 @@ def main():
         res["c2_noncausal"] = bench_flash(args.steps, args.warmup, False)
     if "paged" in parts:
         res["c5_paged"] = bench_paged(args.paged_steps)
+    if "paged_host" in parts:
+        res["c5_host"] = bench_paged_host(args.paged_steps)
     if "decode" in parts:
         res["c4_decode"] = bench_decode(args.steps, args.warmup)
     if "copy" in parts:
@@ -334,6 +398,15 @@ def main():
                          "unit": "GB/s", "frac": round(pg["gbps"] / PEAK_HBM_GBPS, 4),
                          "traffic": load_traffic("paged_c5")},
         }
+    if "c5_host" in res:
+        hp = res["c5_host"]
+        line["paged_decode_host_api"] = {
+            "value": round(hp["gbps"], 1), "unit": "GB/s", "dtype": "bf16",
+            "ms_per_step": round(hp["ms"], 4), "append_batch_and_sync_ms": round(hp["append_sync_ms"], 4),
+            "splits": hp["splits"],
+            "workload": "C5 through PagedKVCache (pages scattered by interleaved appends) and "
+                        "sca::paged_attention; API-inclusive attend time; one AppendTokensBatch "
+                        "+ sparse page-table sync per step timed separately"}
     if "c4_decode" in res:
         d = res["c4_decode"]
         line["splitk_decode"] = {"value": round(d["gbps"], 1), "unit": "GB/s", "dtype": "f16",

@@ -158,6 +158,11 @@ SCA_CAPI ScaPagedKV* sca_pkv_create(const ScaKvConfig* cfg, int32_t device_kind)
 SCA_CAPI void sca_pkv_destroy(ScaPagedKV* c);
 SCA_CAPI int sca_pkv_append(ScaPagedKV* c, int64_t seq_id, int64_t layer, const ScaTensor* k_new,
                             const ScaTensor* v_new, void* stream);
+/* One token per sequence id, in order (sca::PagedKVCache::AppendTokensBatch; no reference
+ * counterpart: the reference appends one sequence per call). */
+SCA_CAPI int sca_pkv_append_batch(ScaPagedKV* c, const int64_t* seq_ids, int64_t num_entries,
+                                  int64_t layer, const ScaTensor* k_new, const ScaTensor* v_new,
+                                  void* stream);
 SCA_CAPI int sca_pkv_reset(ScaPagedKV* c, int64_t seq_id, void* stream);
 SCA_CAPI int sca_pkv_sync(ScaPagedKV* c, void* stream);
 SCA_CAPI int sca_pkv_force_sync(ScaPagedKV* c, void* stream);

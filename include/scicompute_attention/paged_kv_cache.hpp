@@ -47,6 +47,16 @@ public:
     sci::Status AppendTokens(int64_t seq_id, int64_t layer, const sci::Tensor& k_new,
                              const sci::Tensor& v_new, sci::Stream* stream);
 
+    // One decode step for a batch: token i of k_new/v_new ([num_entries, num_kv_heads, head_dim],
+    // device) is appended to sequence seq_ids[i], in order (an id may repeat). No counterpart in
+    // the reference, which appends one sequence per call; the resulting state (pages, their order,
+    // table rows, lengths, revision) equals that of one AppendTokens call per entry in order, but
+    // the slots go up in one copy and the tokens in one scatter launch. All or nothing: when the
+    // pool cannot supply every page the batch needs, nothing changes (kKVCapacityExceeded).
+    sci::Status AppendTokensBatch(const int64_t* seq_ids, int64_t num_entries, int64_t layer,
+                                  const sci::Tensor& k_new, const sci::Tensor& v_new,
+                                  sci::Stream* stream);
+
     // Zeroes the sequence's pages, returns them to the pool and clears its row.
     sci::Status ResetSeq(int64_t seq_id, sci::Stream* stream);
 

@@ -121,6 +121,7 @@ _SIGS = [
     ("sca_pkv_create", c_vp, [ctypes.POINTER(ScaKvConfig), c_i32]),
     ("sca_pkv_destroy", None, [c_vp]),
     ("sca_pkv_append", ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
+    ("sca_pkv_append_batch", ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
     ("sca_pkv_reset", ctypes.c_int, [c_vp, c_i64, c_vp]),
     ("sca_pkv_sync", ctypes.c_int, [c_vp, c_vp]),
     ("sca_pkv_force_sync", ctypes.c_int, [c_vp, c_vp]),
@@ -535,6 +536,12 @@ class PagedKVCache:
 
     def append_tokens(self, seq, layer, k_new: Tensor, v_new: Tensor, stream=None):
         _raise(host_lib().sca_pkv_append(self.h, seq, layer, k_new.handle, v_new.handle, stream))
+
+    def append_batch(self, seq_ids, layer, k_new: Tensor, v_new: Tensor, stream=None):
+        """One token per entry of seq_ids ([n, H_kv, D] device tensors), in order."""
+        ids = np.ascontiguousarray(np.asarray(seq_ids, dtype=np.int64))
+        _raise(host_lib().sca_pkv_append_batch(self.h, ids.ctypes.data, ids.size, layer,
+                                               k_new.handle, v_new.handle, stream))
 
     def reset_seq(self, seq, stream=None):
         _raise(host_lib().sca_pkv_reset(self.h, seq, stream))

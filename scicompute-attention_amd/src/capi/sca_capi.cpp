@@ -327,6 +327,13 @@ int sca_pkv_append(ScaPagedKV* c, int64_t seq_id, int64_t layer, const ScaTensor
     sci::Stream holder;
     return Check(P(c).AppendTokens(seq_id, layer, T(k_new), T(v_new), StreamArg(stream, &holder)));
 }
+int sca_pkv_append_batch(ScaPagedKV* c, const int64_t* seq_ids, int64_t num_entries,
+                         int64_t layer, const ScaTensor* k_new, const ScaTensor* v_new,
+                         void* stream) {
+    sci::Stream holder;
+    return Check(P(c).AppendTokensBatch(seq_ids, num_entries, layer, T(k_new), T(v_new),
+                                        StreamArg(stream, &holder)));
+}
 int sca_pkv_reset(ScaPagedKV* c, int64_t seq_id, void* stream) {
     sci::Stream holder;
     return Check(P(c).ResetSeq(seq_id, StreamArg(stream, &holder)));

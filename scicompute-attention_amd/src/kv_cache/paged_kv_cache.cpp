@@ -268,6 +268,128 @@ sci::Status PagedKVCache::AppendTokens(int64_t seq_id, int64_t layer, const sci:
     return sci::Status::Ok();
 }
 
+sci::Status PagedKVCache::AppendTokensBatch(const int64_t* seq_ids, int64_t num_entries,
+                                            int64_t layer, const sci::Tensor& k_new,
+                                            const sci::Tensor& v_new, sci::Stream* stream) {
+    if (seq_ids == nullptr || num_entries <= 0) {
+        return MakeStatus(AttnStatusCode::kShapeMismatch,
+                          "PagedKVCache::AppendTokensBatch needs at least one sequence id");
+    }
+    if (layer < 0 || layer >= cfg_.num_layers) {
+        return MakeStatus(AttnStatusCode::kShapeMismatch,
+                          "PagedKVCache::AppendTokensBatch layer=" + std::to_string(layer) +
+                              " out of range [0," + std::to_string(cfg_.num_layers) + ")");
+    }
+    if (k_new.ndims() != 3 || v_new.ndims() != 3 || k_new.dim(0) != num_entries ||
+        v_new.dim(0) != num_entries) {
+        return MakeStatus(AttnStatusCode::kShapeMismatch,
+                          "PagedKVCache::AppendTokensBatch expects [num_entries, n_kv_heads, "
+                          "head_dim] tensors with one token per sequence id");
+    }
+    if (k_new.dim(1) != cfg_.num_kv_heads || k_new.dim(2) != cfg_.head_dim ||
+        v_new.dim(1) != cfg_.num_kv_heads || v_new.dim(2) != cfg_.head_dim ||
+        k_new.dtype() != cfg_.dtype || v_new.dtype() != cfg_.dtype) {
+        return MakeStatus(AttnStatusCode::kShapeMismatch,
+                          "PagedKVCache::AppendTokensBatch token shape differs from the cache's [" +
+                              std::to_string(cfg_.num_kv_heads) + ", " +
+                              std::to_string(cfg_.head_dim) + "]");
+    }
+    // Pages the whole batch needs, before anything changes.
+    std::vector<int64_t> lens;   // running lengths of the sequences touched, by first appearance
+    std::vector<int64_t> owned;  // their page counts
+    std::vector<int64_t> index(static_cast<size_t>(num_entries));
+    int64_t missing = 0;
+    for (int64_t i = 0; i < num_entries; ++i) {
+        const int64_t id = seq_ids[i];
+        if (id < 0 || id >= cfg_.max_num_seqs) {
+            return MakeStatus(AttnStatusCode::kShapeMismatch,
+                              "PagedKVCache::AppendTokensBatch seq_id=" + std::to_string(id) +
+                                  " out of range [0," + std::to_string(cfg_.max_num_seqs) + ")");
+        }
+        int64_t k = 0;
+        while (k < i && seq_ids[k] != id) ++k;
+        if (k == i) {
+            index[static_cast<size_t>(i)] = static_cast<int64_t>(lens.size());
+            lens.push_back(seq_lengths_[static_cast<size_t>(id)]);
+            owned.push_back(static_cast<int64_t>(seq_blocks_[static_cast<size_t>(id)].size()));
+        } else {
+            index[static_cast<size_t>(i)] = index[static_cast<size_t>(k)];
+        }
+        const size_t u = static_cast<size_t>(index[static_cast<size_t>(i)]);
+        const int64_t needed = (lens[u] + 1 + cfg_.block_size - 1) / cfg_.block_size;
+        if (needed > owned[u]) {
+            missing += needed - owned[u];
+            owned[u] = needed;
+        }
+        if (needed > max_blocks_per_seq_) {
+            return MakeStatus(AttnStatusCode::kKVCapacityExceeded,
+                              "PagedKVCache::AppendTokensBatch seq=" + std::to_string(id) +
+                                  " would exceed " + std::to_string(max_blocks_per_seq_) +
+                                  " pages");
+        }
+        ++lens[u];
+    }
+    if (missing > blocks_.NumFreeBlocks()) {
+        return MakeStatus(AttnStatusCode::kKVCapacityExceeded,
+                          "PagedKVCache::AppendTokensBatch needs " + std::to_string(missing) +
+                              " more blocks but only " + std::to_string(blocks_.NumFreeBlocks()) +
+                              " are free");
+    }
+    if (slot_mapping_capacity_ < num_entries) {
+        const int64_t capacity = std::max<int64_t>(num_entries, kMinStagingEntries);
+        slot_mapping_device_ = sci::Tensor(sci::TensorShape({capacity}), sci::DType::kInt32,
+                                           page_table_device_.device());
+        if (slot_mapping_device_.data() == nullptr) {
+            slot_mapping_capacity_ = 0;
+            return MakeStatus(AttnStatusCode::kKVCapacityExceeded,
+                              "PagedKVCache: slot-mapping buffer allocation failed");
+        }
+        slot_mapping_capacity_ = capacity;
+    }
+    sci::Result<int32_t*> staging = Staging(num_entries);
+    if (!staging.ok()) return staging.error();
+
+    // Entry by entry, exactly as AppendTokens would: page (if the token opens one), table tail,
+    // slot; lengths and the revision advance per entry.
+    int32_t* slots = *staging;
+    for (int64_t i = 0; i < num_entries; ++i) {
+        const int64_t id = seq_ids[i];
+        const size_t sid = static_cast<size_t>(id);
+        std::vector<int32_t>& pages = seq_blocks_[sid];
+        const int64_t len = seq_lengths_[sid];
+        int32_t* row = page_table_host_.data() + id * max_blocks_per_seq_;
+        if (len / cfg_.block_size >= static_cast<int64_t>(pages.size())) {
+            sci::Result<std::vector<int32_t>> got = blocks_.Allocate(1);
+            if (!got.ok()) return got.error();  // cannot happen: counted above
+            const sci::Status st = blocks_.AppendToTable(id, got->data(), 1);
+            if (!st.ok()) {
+                blocks_.Free(got->data(), 1);
+                return st;
+            }
+            const int64_t pos = static_cast<int64_t>(pages.size());
+            pages.push_back((*got)[0]);
+            row[pos] = (*got)[0];
+            pending_entries_.push_back(id * max_blocks_per_seq_ + pos);
+        }
+        slots[i] = static_cast<int32_t>(static_cast<int64_t>(row[len / cfg_.block_size]) *
+                                            cfg_.block_size +
+                                        len % cfg_.block_size);
+        seq_lengths_[sid] = len + 1;
+        ++revision_;
+        ++num_appends_;
+    }
+    void* s = runtime::StreamHandle(stream);
+    sci::Status st = runtime::StatusFromHip(
+        sca_hip_memcpy_async(slot_mapping_device_.data(), slots,
+                             static_cast<size_t>(num_entries) * sizeof(int32_t), SCA_COPY_H2D, s),
+        "PagedKVCache batch slot upload");
+    if (st.ok()) st = StagingSubmitted(s, stream == nullptr);
+    if (!st.ok()) return st;
+    return storage_.Append(layer, k_new, v_new,
+                           static_cast<const int32_t*>(slot_mapping_device_.data()), num_entries,
+                           stream);
+}
+
 sci::Status PagedKVCache::ResetSeq(int64_t seq_id, sci::Stream* stream) {
     if (seq_id < 0 || seq_id >= cfg_.max_num_seqs) {
         return MakeStatus(AttnStatusCode::kShapeMismatch,

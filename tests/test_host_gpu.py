@@ -184,6 +184,57 @@ def test_paged_cache_state_matches_reference_restatement(hip):
         assert np.array_equal(flat, srv.k[s])
 
 
+def test_batched_append_equals_per_sequence_appends(hip):
+    # One AppendTokensBatch per decode step (ids may repeat) leaves exactly the state of one
+    # AppendTokens call per entry, and the same tokens in the same slots.
+    rng = np.random.default_rng(11)
+    seqs, bs, Hkv, D = 6, 8, 2, 64
+    a = Serving(num_blocks=60, bs=bs, seqs=seqs, Hkv=Hkv, D=D, dtype="bf16")
+    b = Serving(num_blocks=60, bs=bs, seqs=seqs, Hkv=Hkv, D=D, dtype="bf16")
+    for s in range(seqs):
+        n = int(rng.integers(1, 9))
+        assert a.append(s, n, 500 + s) == 0 and b.append(s, n, 500 + s) == 0
+    for step in range(25):
+        ids = rng.integers(0, seqs, size=int(rng.integers(1, 9)))
+        k = uniform((len(ids), Hkv, D), 900 + step)
+        v = uniform((len(ids), Hkv, D), 950 + step)
+        (kb, _), (vb, _) = quantize(k, "bf16"), quantize(v, "bf16")
+        a.cache.append_batch(ids, 0, tensor(kb, "bf16"), tensor(vb, "bf16"))
+        for i, s in enumerate(ids):
+            b.cache.append_tokens(int(s), 0, tensor(kb[i:i + 1].copy(), "bf16"),
+                                  tensor(vb[i:i + 1].copy(), "bf16"))
+        assert np.array_equal(a.cache.page_table_host(), b.cache.page_table_host())
+        for s in range(seqs):
+            assert a.cache.seq_length(s) == b.cache.seq_length(s)
+            assert a.cache.logical_block_count(s) == b.cache.logical_block_count(s)
+        assert a.cache.revision == b.cache.revision
+        sa, sb = a.cache.stats(), b.cache.stats()
+        for key in ("used_blocks", "free_blocks", "num_appends", "num_resets"):
+            assert sa[key] == sb[key], key
+    pt = a.cache.page_table_host()
+    for s in range(seqs):
+        n = a.cache.logical_block_count(s)
+        ids = tensor(pt[s, :n].copy(), "i32")
+        ga = a.cache.gather(True, 0, ids.data_ptr, n).numpy()
+        gb = b.cache.gather(True, 0, ids.data_ptr, n).numpy()
+        L = a.cache.seq_length(s)
+        assert np.array_equal(ga.reshape(n * bs, -1)[:L], gb.reshape(n * bs, -1)[:L])
+        va = a.cache.gather(False, 0, ids.data_ptr, n).numpy()
+        vb_ = b.cache.gather(False, 0, ids.data_ptr, n).numpy()
+        assert np.array_equal(va.reshape(n * bs, -1)[:L], vb_.reshape(n * bs, -1)[:L])
+    # A batch the pool cannot hold changes nothing.
+    before = (a.cache.page_table_host().copy(), a.cache.revision,
+              [a.cache.seq_length(s) for s in range(seqs)])
+    free = a.cache.stats()["free_blocks"]
+    big = np.repeat(np.arange(seqs), (free + 2) * bs // seqs + bs)
+    z = tensor(np.zeros((len(big), Hkv, D), np.uint16), "bf16")
+    with pytest.raises(H.ScaError) as e:
+        a.cache.append_batch(big, 0, z, z)
+    assert e.value.code == 2007
+    assert np.array_equal(a.cache.page_table_host(), before[0]) and a.cache.revision == before[1]
+    assert [a.cache.seq_length(s) for s in range(seqs)] == before[2]
+
+
 def test_paged_cache_errors_leave_state_unchanged(hip):
     srv = Serving(num_blocks=2, bs=8, seqs=4, Hkv=1, D=32, dtype="f16")
     assert srv.append(0, 16, 1) == 0
