@@ -151,6 +151,46 @@ SCA_HIP_API int sca_hip_flash_tile(int32_t head_dim, int32_t* block_m, int32_t* 
                                    int32_t* waves, int32_t* stages);
 SCA_HIP_API int sca_hip_flash_fwd(const sca_flash_params* params, void* stream);
 
+/* Packed variable-length prefill in one launch (no reference counterpart: the reference's
+ * FlashBackend::ForwardVarlen, flash_backend.cpp:226-376, launches once per sequence).
+ * q/out are packed [T_q, H_q, D] and k/v [T_kv, H_kv, D] (token stride *_ss, head stride *_sh);
+ * sequence s spans tokens [cu_seqlens_q[s], cu_seqlens_q[s+1]) and likewise for k/v. `tiles` is
+ * the device copy of the work list sca_hip_flash_varlen_tiles writes (2 int32 per 128-row tile:
+ * sequence, row tile; longest first). head_dim 64 or 128 (other head dims: launch per sequence).
+ * Causal masking is bottom-right per sequence (key j visible from row i iff j <= i + S_kv - S_q). */
+typedef struct sca_flash_varlen_params {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    const int32_t* cu_seqlens_q;  /* device, num_seqs + 1 */
+    const int32_t* cu_seqlens_kv; /* device, num_seqs + 1 */
+    const int32_t* tiles;         /* device, 2 * num_tiles */
+    int64_t num_seqs;
+    int64_t num_tiles;
+    int64_t max_seq_kv;
+    int64_t num_heads;
+    int64_t num_kv_heads;
+    int64_t head_dim;
+    int64_t q_sh, q_ss;
+    int64_t k_sh, k_ss;
+    int64_t v_sh, v_ss;
+    int64_t o_sh, o_ss;
+    float scale;
+    int32_t causal;
+    int32_t dtype;                /* SCA_DTYPE_F16 or SCA_DTYPE_BF16 */
+} sca_flash_varlen_params;
+
+/* Work list of a packed launch from host cu_seqlens: writes 2 int32 per row tile (sequence, tile)
+ * into tiles_out (may be NULL to count only), ordered by decreasing key count; returns the tile
+ * count, or a negative status when the lengths are invalid. */
+SCA_HIP_API int64_t sca_hip_flash_varlen_tiles(const int32_t* cu_seqlens_q,
+                                               const int32_t* cu_seqlens_kv, int64_t num_seqs,
+                                               int32_t causal, int32_t* tiles_out);
+/* 1 when head_dim has the one-launch varlen kernel. */
+SCA_HIP_API int sca_hip_flash_varlen_supported(int32_t head_dim);
+SCA_HIP_API int sca_hip_flash_fwd_varlen(const sca_flash_varlen_params* params, void* stream);
+
 /* ------------------------------------------------------------------------------------------- */
 /* split-K decode (contiguous and paged)                                                        */
 /* replaces: src/backends/decode/decode_splitk.cuh:15-57 (DecodeFwdParams, LaunchDecodeSplitK,  */

@@ -26,7 +26,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
+#include <algorithm>
 #include <string>
+#include <vector>
 
 #include "sca_device.hpp"
 
@@ -528,9 +530,17 @@ __device__ __forceinline__ void DmaToLds(const uint8_t* base, int num_records, u
                                              voffset, soffset, 0, 0);
 }
 
-template <typename E, int D, int RG, int KQ, bool kCausal>
+// Packed variable-length launch: cumulative token offsets and the work list (2 int32 per row
+// tile: sequence, tile), device-resident.
+struct VarlenArgs {
+    const int32_t* cu_q;
+    const int32_t* cu_kv;
+    const int32_t* tiles;
+};
+
+template <typename E, int D, int RG, int KQ, bool kCausal, bool kVarlen>
 __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dma_kernel(
-    const sca_flash_params p, int num_q_tiles) {
+    const sca_flash_params p, int num_q_tiles, const VarlenArgs va) {
     using G = DmaGeom<D, RG, KQ>;
     constexpr bool kRing4 = G::kRing4;
     using M = Mfma<E>;
@@ -560,6 +570,21 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     const int64_t b = bh / p.num_heads;
     const int64_t h = bh % p.num_heads;
     const int64_t h_kv = h / (p.num_heads / p.num_kv_heads);
+    // Sequence geometry: the b-th sequence of the batch, or for a packed varlen launch the
+    // sequence and row tile of work entry tile_linear (tok_*: its first token in the packing).
+    int64_t tok_q = 0, tok_kv = 0, var_qt = 0;
+    int wg_seq_q = static_cast<int>(p.seq_q);
+    int wg_seq_kv = static_cast<int>(p.seq_kv);
+    int wg_diag = static_cast<int>(p.diagonal);
+    if constexpr (kVarlen) {
+        const int seq = va.tiles[2 * tile_linear];
+        var_qt = va.tiles[2 * tile_linear + 1];
+        tok_q = va.cu_q[seq];
+        tok_kv = va.cu_kv[seq];
+        wg_seq_q = va.cu_q[seq + 1] - static_cast<int>(tok_q);
+        wg_seq_kv = va.cu_kv[seq + 1] - static_cast<int>(tok_kv);
+        wg_diag = kCausal ? wg_seq_kv - wg_seq_q : 0;
+    }
     // Causal split-slot workgroups run row tiles t = tile_linear and T-1-t (largest first).
     constexpr bool kPaired = kCausal && !kRing4;
     const int passes = kPaired ? ((2 * tile_linear + 1 < num_q_tiles) ? 2 : 1) : 1;
@@ -568,15 +593,16 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     const int q0 = static_cast<int>(qt) * BM;
     const int wave_q0 = q0 + rg * kRowsPerWave;
     const int my_q = wave_q0 + lr;
-    const int seq_q = static_cast<int>(p.seq_q);
-    const int seq_kv = static_cast<int>(p.seq_kv);
-    const int diag = static_cast<int>(p.diagonal);
+    const int seq_q = wg_seq_q;
+    const int seq_kv = wg_seq_kv;
+    const int diag = wg_diag;
 
-    const uint16_t* q_ptr = static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh;
-    const uint8_t* k_bytes =
-        reinterpret_cast<const uint8_t*>(static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh);
-    const uint8_t* v_bytes =
-        reinterpret_cast<const uint8_t*>(static_cast<const uint16_t*>(p.v) + b * p.v_sb + h_kv * p.v_sh);
+    const uint16_t* q_ptr =
+        static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh + tok_q * p.q_ss;
+    const uint8_t* k_bytes = reinterpret_cast<const uint8_t*>(
+        static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh + tok_kv * p.k_ss);
+    const uint8_t* v_bytes = reinterpret_cast<const uint8_t*>(
+        static_cast<const uint16_t*>(p.v) + b * p.v_sb + h_kv * p.v_sh + tok_kv * p.v_ss);
     const int k_row_bytes = static_cast<int>(p.k_ss) * 2;
     const int v_row_bytes = static_cast<int>(p.v_ss) * 2;
 
@@ -911,7 +937,7 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (my_q < seq_q) {
         uint16_t* out_row = static_cast<uint16_t*>(p.out) + b * p.o_sb + h * p.o_sh +
-                            static_cast<int64_t>(my_q) * p.o_ss;
+                            (tok_q + my_q) * p.o_ss;
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) {
 #pragma unroll
@@ -936,6 +962,8 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
             __syncthreads();  // the first tile's merge buffer is the second tile's ring
             run_tile(tile_linear);
         }
+    } else if constexpr (kVarlen) {
+        run_tile(var_qt);
     } else {
         run_tile(kCausal ? num_q_tiles - 1 - tile_linear : tile_linear);
     }
@@ -964,13 +992,14 @@ int LaunchFlashDma(const sca_flash_params& p, hipStream_t s) {
     static bool attr_set = false;
     if (!attr_set) {
         const hipError_t err = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&flash_fwd_dma_kernel<E, D, RG, KQ, kCausal>),
+            reinterpret_cast<const void*>(&flash_fwd_dma_kernel<E, D, RG, KQ, kCausal, false>),
             hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
         if (err != hipSuccess) (void)hipGetLastError();
         attr_set = true;
     }
-    hipLaunchKernelGGL((flash_fwd_dma_kernel<E, D, RG, KQ, kCausal>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(G::THREADS), G::LDS_BYTES, s, p, static_cast<int>(num_q_tiles));
+    hipLaunchKernelGGL((flash_fwd_dma_kernel<E, D, RG, KQ, kCausal, false>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(G::THREADS), G::LDS_BYTES, s, p,
+                       static_cast<int>(num_q_tiles), VarlenArgs{nullptr, nullptr, nullptr});
     return CheckLaunch("flash_fwd_dma_kernel", s);
 }
 
@@ -1045,6 +1074,62 @@ int LaunchForDim(const sca_flash_params& p, hipStream_t s) {
 
 bool Aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
+// One launch over a packed batch: the 128-row geometry, one workgroup per (work entry, head).
+template <typename E, int D, bool kCausal>
+int LaunchFlashVarlen(const sca_flash_varlen_params& v, hipStream_t s) {
+    using G = DmaGeom<D, 4, 2>;
+    const int64_t rows_k = v.max_seq_kv + 4 * G::BN;
+    if (rows_k * v.k_ss * 2 >= (1LL << 31) || rows_k * v.v_ss * 2 >= (1LL << 31)) {
+        return SetError(SCA_E_SEQ_TOO_LONG, "flash varlen: a sequence of " +
+                                                std::to_string(v.max_seq_kv) +
+                                                " keys exceeds the 32-bit tile offsets");
+    }
+    const int64_t blocks = v.num_tiles * v.num_heads;
+    if (blocks <= 0) return 0;
+    if (blocks > 0x7fffffffLL) {
+        return SetError(SCA_E_SEQ_TOO_LONG, "flash varlen: grid too large");
+    }
+    sca_flash_params p{};
+    p.q = v.q;
+    p.k = v.k;
+    p.v = v.v;
+    p.out = v.out;
+    p.lse = nullptr;
+    p.batch = 1;
+    p.num_heads = v.num_heads;
+    p.num_kv_heads = v.num_kv_heads;
+    p.head_dim = v.head_dim;
+    p.q_sh = v.q_sh, p.q_ss = v.q_ss;
+    p.k_sh = v.k_sh, p.k_ss = v.k_ss;
+    p.v_sh = v.v_sh, p.v_ss = v.v_ss;
+    p.o_sh = v.o_sh, p.o_ss = v.o_ss;
+    p.scale = v.scale;
+    p.causal = v.causal;
+    p.dtype = v.dtype;
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t err = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&flash_fwd_dma_kernel<E, D, 4, 2, kCausal, true>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
+        if (err != hipSuccess) (void)hipGetLastError();
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((flash_fwd_dma_kernel<E, D, 4, 2, kCausal, true>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(G::THREADS), G::LDS_BYTES, s, p,
+                       0, VarlenArgs{v.cu_seqlens_q, v.cu_seqlens_kv, v.tiles});
+    return CheckLaunch("flash_fwd_dma_kernel (varlen)", s);
+}
+
+template <typename E>
+int LaunchVarlenTyped(const sca_flash_varlen_params& v, hipStream_t s) {
+    if (v.head_dim == 64) {
+        return v.causal ? LaunchFlashVarlen<E, 64, true>(v, s) : LaunchFlashVarlen<E, 64, false>(v, s);
+    }
+    return v.causal ? LaunchFlashVarlen<E, 128, true>(v, s) : LaunchFlashVarlen<E, 128, false>(v, s);
+}
+
+
+
 int LdsBytesFor(int64_t head_dim) {
     switch (head_dim) {
         case 32: return FlashGeom<32>::LDS_BYTES;
@@ -1102,6 +1187,74 @@ int sca_hip_flash_tile(int32_t head_dim, int32_t* block_m, int32_t* block_n, int
     if (waves != nullptr) *waves = nw;
     if (stages != nullptr) *stages = ns;
     return 0;
+}
+
+int sca_hip_flash_varlen_supported(int32_t head_dim) { return head_dim == 64 || head_dim == 128; }
+
+int64_t sca_hip_flash_varlen_tiles(const int32_t* cu_q, const int32_t* cu_kv, int64_t num_seqs,
+                                   int32_t causal, int32_t* tiles_out) {
+    if (cu_q == nullptr || cu_kv == nullptr || num_seqs < 1) {
+        return -SetError(SCA_E_SHAPE_MISMATCH, "flash varlen: null cu_seqlens or no sequences");
+    }
+    constexpr int64_t kRows = 128;  // rows per workgroup of the varlen launch
+    struct Tile {
+        int64_t keys;
+        int32_t seq;
+        int32_t tile;
+    };
+    std::vector<Tile> tiles;
+    for (int64_t s = 0; s < num_seqs; ++s) {
+        const int64_t sq = static_cast<int64_t>(cu_q[s + 1]) - cu_q[s];
+        const int64_t skv = static_cast<int64_t>(cu_kv[s + 1]) - cu_kv[s];
+        if (sq < 0 || skv < 0 || (causal && skv < sq) || (sq > 0 && skv == 0)) {
+            return -SetError(SCA_E_SHAPE_MISMATCH,
+                             "flash varlen: sequence " + std::to_string(s) + " has S_q=" +
+                                 std::to_string(sq) + ", S_kv=" + std::to_string(skv));
+        }
+        for (int64_t t = 0; t * kRows < sq; ++t) {
+            const int64_t last = std::min(sq, (t + 1) * kRows) - 1 + (skv - sq);
+            const int64_t keys = causal ? std::min(skv, last + 1) : skv;
+            tiles.push_back({keys, static_cast<int32_t>(s), static_cast<int32_t>(t)});
+        }
+    }
+    std::stable_sort(tiles.begin(), tiles.end(),
+                     [](const Tile& a, const Tile& b) { return a.keys > b.keys; });
+    if (tiles_out != nullptr) {
+        for (size_t i = 0; i < tiles.size(); ++i) {
+            tiles_out[2 * i] = tiles[i].seq;
+            tiles_out[2 * i + 1] = tiles[i].tile;
+        }
+    }
+    return static_cast<int64_t>(tiles.size());
+}
+
+int sca_hip_flash_fwd_varlen(const sca_flash_varlen_params* v, void* stream) {
+    if (v == nullptr || v->q == nullptr || v->k == nullptr || v->v == nullptr ||
+        v->out == nullptr || v->cu_seqlens_q == nullptr || v->cu_seqlens_kv == nullptr ||
+        (v->num_tiles > 0 && v->tiles == nullptr)) {
+        return SetError(SCA_E_SHAPE_MISMATCH, "flash varlen: null pointer");
+    }
+    if (!sca_hip_flash_varlen_supported(static_cast<int32_t>(v->head_dim))) {
+        return SetError(SCA_E_UNSUPPORTED_HEAD_DIM,
+                        "flash varlen: head_dim=" + std::to_string(v->head_dim) +
+                            " has no one-launch kernel (64 and 128 do)");
+    }
+    if (v->dtype != SCA_DTYPE_F16 && v->dtype != SCA_DTYPE_BF16) {
+        return SetError(SCA_E_UNSUPPORTED_DTYPE, "flash varlen: fp16/bf16 only");
+    }
+    if (v->num_heads < 1 || v->num_kv_heads < 1 || v->num_heads % v->num_kv_heads != 0 ||
+        v->num_tiles < 0 || v->max_seq_kv < 0 || v->num_seqs < 1) {
+        return SetError(SCA_E_SHAPE_MISMATCH, "flash varlen: invalid heads or counts");
+    }
+    if (!sca_hip::Aligned16(v->q) || !sca_hip::Aligned16(v->k) || !sca_hip::Aligned16(v->v) ||
+        !sca_hip::Aligned16(v->out) || v->q_ss % 8 || v->q_sh % 8 || v->k_ss % 8 ||
+        v->k_sh % 8 || v->v_ss % 8 || v->v_sh % 8 || v->o_ss % 8 || v->o_sh % 8) {
+        return SetError(SCA_E_LAYOUT_MISMATCH,
+                        "flash varlen: pointers must be 16 B aligned and strides multiples of 8");
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return v->dtype == SCA_DTYPE_F16 ? sca_hip::LaunchVarlenTyped<sca_hip::F16>(*v, s)
+                                     : sca_hip::LaunchVarlenTyped<sca_hip::BF16>(*v, s);
 }
 
 int sca_hip_flash_fwd(const sca_flash_params* p, void* stream) {

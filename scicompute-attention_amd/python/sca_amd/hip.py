@@ -63,6 +63,18 @@ class FlashParams(ctypes.Structure):
     ]
 
 
+class FlashVarlenParams(ctypes.Structure):
+    _fields_ = [
+        ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp),
+        ("cu_seqlens_q", c_vp), ("cu_seqlens_kv", c_vp), ("tiles", c_vp),
+        ("num_seqs", c_i64), ("num_tiles", c_i64), ("max_seq_kv", c_i64),
+        ("num_heads", c_i64), ("num_kv_heads", c_i64), ("head_dim", c_i64),
+        ("q_sh", c_i64), ("q_ss", c_i64), ("k_sh", c_i64), ("k_ss", c_i64),
+        ("v_sh", c_i64), ("v_ss", c_i64), ("o_sh", c_i64), ("o_ss", c_i64),
+        ("scale", ctypes.c_float), ("causal", c_i32), ("dtype", c_i32),
+    ]
+
+
 class DecodeParams(ctypes.Structure):
     _fields_ = [
         ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp),
@@ -117,6 +129,10 @@ def hip_lib() -> ctypes.CDLL:
     lib.sca_hip_flash_lds_bytes.restype = c_i64
     lib.sca_hip_flash_tile.argtypes = [c_i32] + [ctypes.POINTER(c_i32)] * 4
     lib.sca_hip_flash_fwd.argtypes = [ctypes.POINTER(FlashParams), c_vp]
+    lib.sca_hip_flash_varlen_tiles.argtypes = [c_vp, c_vp, c_i64, c_i32, c_vp]
+    lib.sca_hip_flash_varlen_tiles.restype = c_i64
+    lib.sca_hip_flash_varlen_supported.argtypes = [c_i32]
+    lib.sca_hip_flash_fwd_varlen.argtypes = [ctypes.POINTER(FlashVarlenParams), c_vp]
     lib.sca_hip_decode_partial_elements.argtypes = [c_i64] * 4
     lib.sca_hip_decode_partial_elements.restype = c_i64
     lib.sca_hip_decode_splitk.argtypes = [ctypes.POINTER(DecodeParams), c_vp]
@@ -228,6 +244,25 @@ class Event:
 
 def flash_fwd(params: FlashParams, stream=None) -> None:
     check(hip_lib().sca_hip_flash_fwd(ctypes.byref(params), stream))
+
+
+def flash_varlen_tiles(cu_q: np.ndarray, cu_kv: np.ndarray, causal: bool) -> np.ndarray:
+    """Work list (rows of (sequence, row tile), longest first) for a packed launch."""
+    cu_q = np.ascontiguousarray(cu_q, np.int32)
+    cu_kv = np.ascontiguousarray(cu_kv, np.int32)
+    lib = hip_lib()
+    n = lib.sca_hip_flash_varlen_tiles(cu_q.ctypes.data, cu_kv.ctypes.data, len(cu_q) - 1,
+                                       int(causal), None)
+    if n < 0:
+        check(int(-n))
+    out = np.zeros(2 * n, np.int32)
+    lib.sca_hip_flash_varlen_tiles(cu_q.ctypes.data, cu_kv.ctypes.data, len(cu_q) - 1,
+                                   int(causal), out.ctypes.data)
+    return out.reshape(n, 2)
+
+
+def flash_fwd_varlen(params: FlashVarlenParams, stream=None) -> None:
+    check(hip_lib().sca_hip_flash_fwd_varlen(ctypes.byref(params), stream))
 
 
 def decode_splitk(params: DecodeParams, stream=None) -> None:

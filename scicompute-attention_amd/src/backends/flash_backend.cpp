@@ -5,6 +5,8 @@
 // Guarantees: the S_q x S_kv score matrix never reaches HBM (workspace_bytes == 0 and
 // materialized_score_bytes == 0 on every result).
 
+#include <algorithm>
+#include <vector>
 #include <string>
 
 #include "runtime/internal.hpp"
@@ -253,6 +255,60 @@ public:
         const int64_t kv_token = num_kv_heads * head_dim;
         const float scale = EffectiveScale(cfg, probe);
         void* stream = runtime::StreamHandle(cfg.stream);
+        if (sca_hip_flash_varlen_supported(static_cast<int32_t>(head_dim))) {
+            // One launch over the whole packing: cu_seqlens and the longest-first tile list go
+            // up together into a scratch buffer.
+            const int32_t causal = cfg.causal ? 1 : 0;
+            const int64_t n_tiles =
+                sca_hip_flash_varlen_tiles(cu_q, cu_kv, num_seqs, causal, nullptr);
+            if (n_tiles < 0) {
+                return fail(AttnStatusCode::kShapeMismatch, sca_hip_last_error_string());
+            }
+            std::vector<int32_t> table(static_cast<size_t>(2 * (num_seqs + 1) + 2 * n_tiles));
+            std::copy(cu_q, cu_q + num_seqs + 1, table.begin());
+            std::copy(cu_kv, cu_kv + num_seqs + 1, table.begin() + (num_seqs + 1));
+            sca_hip_flash_varlen_tiles(cu_q, cu_kv, num_seqs, causal,
+                                       table.data() + 2 * (num_seqs + 1));
+            int64_t max_kv = 0;
+            for (int64_t s = 0; s < num_seqs; ++s) {
+                max_kv = std::max<int64_t>(max_kv, cu_kv[s + 1] - cu_kv[s]);
+            }
+            sci::Result<void*> dev =
+                runtime::UploadToScratch(runtime::ScratchKind::kVarlenTables, table.data(),
+                                         table.size() * sizeof(int32_t), q.device().id(), stream);
+            if (!dev.ok()) return sci::MakeUnexpected<AttentionResult>(dev.error());
+            const int32_t* d = static_cast<const int32_t*>(*dev);
+            sca_flash_varlen_params vp{};
+            vp.q = q.data();
+            vp.k = k.data();
+            vp.v = v.data();
+            vp.out = result.out.data();
+            vp.cu_seqlens_q = d;
+            vp.cu_seqlens_kv = d + (num_seqs + 1);
+            vp.tiles = d + 2 * (num_seqs + 1);
+            vp.num_seqs = num_seqs;
+            vp.num_tiles = n_tiles;
+            vp.max_seq_kv = max_kv;
+            vp.num_heads = num_heads;
+            vp.num_kv_heads = num_kv_heads;
+            vp.head_dim = head_dim;
+            vp.q_sh = head_dim, vp.q_ss = q_token;
+            vp.k_sh = head_dim, vp.k_ss = kv_token;
+            vp.v_sh = head_dim, vp.v_ss = kv_token;
+            vp.o_sh = head_dim, vp.o_ss = q_token;
+            vp.scale = scale;
+            vp.causal = causal;
+            vp.dtype = runtime::KernelDtype(q.dtype());
+            const sci::Status status = runtime::StatusFromHip(
+                sca_hip_flash_fwd_varlen(&vp, stream), "flash varlen forward");
+            if (!status.ok()) return sci::MakeUnexpected<AttentionResult>(status);
+            const TileConfig tile = RecommendTile(cfg, probe);
+            FillStats(&result.stats, tile,
+                      "varlen: one launch over " + std::to_string(num_seqs) + " packed sequences, " +
+                          std::to_string(n_tiles) + " row tiles longest first (tile " +
+                          tile.ToString() + ")");
+            return sci::Ok(std::move(result));
+        }
         for (int64_t s = 0; s < num_seqs; ++s) {
             const int64_t sq = cu_q[s + 1] - cu_q[s];
             const int64_t skv = cu_kv[s + 1] - cu_kv[s];

@@ -50,10 +50,14 @@ const IAttentionBackend* PagedBackendInstance() noexcept;
 // One FP32 scratch buffer per (device, kind), grown by 25% + 1024 elements when a request does
 // not fit and otherwise reused; the pointer stays valid until the next acquisition of the same
 // (device, kind). Calls are expected not to overlap (single-threaded use of the API).
-enum class ScratchKind : int { kScoresFp32 = 0, kDecodePartials = 1, kGeneric = 2 };
+enum class ScratchKind : int { kScoresFp32 = 0, kDecodePartials = 1, kGeneric = 2, kVarlenTables = 3 };
 sci::Result<float*> AcquireScratchFp32(ScratchKind kind, size_t elements, int device_id);
 sci::Status ReleaseScratch();
 size_t ScratchHighWaterMarkBytes();
+// Copies `bytes` of host data into the (device, kind) scratch buffer on `stream`, through pinned
+// staging that is reused once the previous copy has completed; returns the device pointer.
+sci::Result<void*> UploadToScratch(ScratchKind kind, const void* host, size_t bytes,
+                                   int device_id, void* stream);
 
 }  // namespace runtime
 }  // namespace sca

@@ -2,12 +2,14 @@
 // Growth rule as in the reference's src/runtime/scratch_pool.cpp:38-60 (x1.25 + 1024 elements).
 
 #include <algorithm>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <utility>
 
 #include "device/device.hpp"
 #include "runtime/internal.hpp"
+#include "sca_hip.h"
 
 namespace sca {
 namespace runtime {
@@ -81,6 +83,66 @@ sci::Status ReleaseScratch() {
 size_t ScratchHighWaterMarkBytes() {
     std::lock_guard<std::mutex> lock(PoolMutex());
     return g_high_water_bytes;
+}
+
+}  // namespace runtime
+}  // namespace sca
+
+namespace sca {
+namespace runtime {
+namespace {
+
+struct Staging {
+    void* host{nullptr};
+    size_t bytes{0};
+    void* event{nullptr};  // recorded after the last copy out of `host`
+};
+
+std::mutex& StagingMutex() {
+    static std::mutex mu;
+    return mu;
+}
+
+std::map<int, Staging>& StagingPool() {  // leaked on purpose, like the scratch pool
+    static auto* pool = new std::map<int, Staging>();
+    return *pool;
+}
+
+}  // namespace
+
+sci::Result<void*> UploadToScratch(ScratchKind kind, const void* host, size_t bytes,
+                                   int device_id, void* stream) {
+    sci::Result<float*> dst = AcquireScratchFp32(kind, (bytes + 3) / 4, device_id);
+    if (!dst.ok()) return sci::MakeUnexpected<void*>(dst.error());
+    std::lock_guard<std::mutex> lock(StagingMutex());
+    Staging& st = StagingPool()[device_id];
+    if (st.event != nullptr) {
+        const sci::Status done =
+            StatusFromHip(sca_hip_event_synchronize(st.event), "scratch staging reuse");
+        if (!done.ok()) return sci::MakeUnexpected<void*>(done);
+    } else {
+        const sci::Status made =
+            StatusFromHip(sca_hip_event_create(&st.event), "scratch staging event");
+        if (!made.ok()) return sci::MakeUnexpected<void*>(made);
+    }
+    if (st.bytes < bytes) {
+        if (st.host != nullptr) sca_hip_host_free(st.host);
+        st.host = nullptr;
+        st.bytes = 0;
+        const size_t grown = std::max<size_t>(bytes, 4096);
+        const sci::Status got =
+            StatusFromHip(sca_hip_host_malloc(&st.host, grown), "scratch staging allocation");
+        if (!got.ok()) return sci::MakeUnexpected<void*>(got);
+        st.bytes = grown;
+    }
+    std::memcpy(st.host, host, bytes);
+    sci::Status status = StatusFromHip(
+        sca_hip_memcpy_async(*dst, st.host, bytes, SCA_COPY_H2D, stream), "scratch upload");
+    if (status.ok()) {
+        status = StatusFromHip(sca_hip_event_record(st.event, stream), "scratch staging event");
+    }
+    if (!status.ok()) return sci::MakeUnexpected<void*>(status);
+    return sci::Ok(static_cast<void*>(*dst));
 }
 
 }  // namespace runtime

@@ -159,3 +159,53 @@ def test_baseline_c3_ragged_tail(hip, seq):
     out, _ = run_flash(qb, kb, vb, "bf16", True, B=B, Hq=Hq, Hkv=Hkv, Sq=seq, Skv=seq, D=D)
     ref, _ = orc.reference_attention(qd, kd, vd, True)
     check_attention(out.reshape(-1, D), ref, "bf16", f"C3 ragged S={seq}")
+
+
+def _varlen_case(dtype, causal, lens_q, lens_kv, Hq, Hkv, D, seed):
+    """One packed launch (sca_hip_flash_fwd_varlen) checked sequence by sequence."""
+    import sca_amd
+    from sca_amd import hip as H
+    from attn_util import to_float
+    Tq, Tkv = int(sum(lens_q)), int(sum(lens_kv))
+    q = uniform((Tq, Hq, D), seed)
+    k = uniform((Tkv, Hkv, D), seed + 7919)
+    v = uniform((Tkv, Hkv, D), seed + 104729)
+    (qb, qd), (kb, kd), (vb, vd) = quantize(q, dtype), quantize(k, dtype), quantize(v, dtype)
+    cu_q = np.concatenate([[0], np.cumsum(lens_q)]).astype(np.int32)
+    cu_kv = np.concatenate([[0], np.cumsum(lens_kv)]).astype(np.int32)
+    tiles = H.flash_varlen_tiles(cu_q, cu_kv, causal)
+    bufs = [H.DeviceBuffer.from_array(a) for a in (qb, kb, vb, cu_q, cu_kv, tiles)]
+    dout = H.DeviceBuffer.zeros(Tq * Hq * D * 2)
+    p = H.FlashVarlenParams()
+    p.q, p.k, p.v, p.out = bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, dout.ptr
+    p.cu_seqlens_q, p.cu_seqlens_kv, p.tiles = bufs[3].ptr, bufs[4].ptr, bufs[5].ptr
+    p.num_seqs, p.num_tiles, p.max_seq_kv = len(lens_q), len(tiles), int(max(lens_kv))
+    p.num_heads, p.num_kv_heads, p.head_dim = Hq, Hkv, D
+    p.q_sh, p.q_ss, p.k_sh, p.k_ss = D, Hq * D, D, Hkv * D
+    p.v_sh, p.v_ss, p.o_sh, p.o_ss = D, Hkv * D, D, Hq * D
+    p.scale = float(np.float32(1.0 / np.sqrt(D)))
+    p.causal = int(causal)
+    p.dtype = H.DTYPE_F16 if dtype == "f16" else H.DTYPE_BF16
+    H.flash_fwd_varlen(p)
+    sca_amd.synchronize()
+    out = to_float(dout.download(np.uint16), dtype).reshape(Tq, Hq, D)
+    tag = f"varlen {dtype} causal={causal} lens_q={list(lens_q)[:6]} D={D}"
+    print(tag, flush=True)
+    for s in range(len(lens_q)):
+        sq = slice(cu_q[s], cu_q[s + 1])
+        skv = slice(cu_kv[s], cu_kv[s + 1])
+        ref, _ = orc.reference_attention(qd[sq].transpose(1, 0, 2)[None],
+                                         kd[skv].transpose(1, 0, 2)[None],
+                                         vd[skv].transpose(1, 0, 2)[None], causal)
+        got = out[sq].transpose(1, 0, 2).reshape(-1, D)
+        check_attention(got, ref.reshape(-1, D), dtype, f"{tag} seq {s}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_one_launch(hip, D, causal):
+    lens_q = [1, 7, 63, 1000, 64, 65, 129, 300]
+    lens_kv = [1, 7, 63, 1000, 64, 65, 129, 300] if causal else [5, 700, 63, 1000, 64, 1, 200, 301]
+    _varlen_case("f16", causal, lens_q, lens_kv, 8, 8, D, 61000 + D + int(causal))
+    # GQA, bf16, S_kv > S_q (bottom-right diagonal per sequence)
+    _varlen_case("bf16", causal, [96, 3, 257], [160, 40, 400], 8, 2, D, 62000 + D + int(causal))
