@@ -10,15 +10,19 @@
 // The partial scratch layout is the reference's: m | l | O with flat index ((b*H_q)+h)*splits+s,
 // m in natural-log units.
 //
-// MI355X design (HBM-bound kernel):
-//   * one workgroup per (b, kv head, split) streams its K/V chunk exactly once and serves all
-//     kHeads query heads of the GQA group from registers (the reference re-reads K/V per q head);
-//   * a lane owns 16 B of one token row (8 fp16/bf16 elements); LPR lanes cover a row, so a wave
-//     reads 64 lanes x 16 B of consecutive token rows per load instruction;
-//   * QK uses v_dot2_f32_{f16,bf16} on the packed inputs, the 16-lane row sum uses DPP,
-//     and the online softmax is updated once per chunk of kChunk tokens per row group;
-//   * row groups and waves are merged in registers / LDS at the end; splits == 1 writes the
-//     normalised output directly and skips the combine kernel.
+// MI355X design (HBM-bound kernels):
+//   * fp16/bf16 with head_dim 64 or 128 (power-of-two page sizes when paged) run
+//     decode_mfma_kernel: the query heads of a GQA group are the 16 columns of
+//     v_mfma_f32_16x16x32 tiles, K goes straight into A-operand registers, V through a small LDS
+//     ring read with transposed loads; ragged batches run longest sequence first. Described at
+//     its definition;
+//   * every other shape (fp32, other head dims) runs decode_partial_kernel: one workgroup per
+//     (b, kv head, split) streams its K/V chunk exactly once and serves kHeads query heads of the
+//     group from registers; a lane owns 16 B of one token row (8 fp16/bf16 elements), QK uses
+//     v_dot2_f32_{f16,bf16} and a DPP row sum, the online softmax is updated once per chunk of
+//     kChunk tokens per row group, and row groups and waves are merged in registers / LDS;
+//   * splits == 1 writes the normalised output directly and skips the combine kernel, which
+//     otherwise runs one thread per (b, h, 4 dims).
 
 #include <hip/hip_runtime.h>
 
@@ -458,7 +462,9 @@ constexpr int kRankBatch = 256;  // ragged batches up to this size are ranked in
 // two-stage ring per wave (one LDS object per stage, so the compiler's LDS-DMA tracking waits
 // only for the stage being read); V rows XOR their 32-byte segments so the transposed reads
 // hit distinct banks. A wave always has the next tile in flight while it computes, and the
-// 64 KB ring lets two workgroups share a CU.
+// 64 KB ring lets two workgroups share a CU. The probabilities are rounded to fp16/bf16 for the
+// PV MFMA (the reference's decode kernel keeps them in fp32; the denominator here sums the
+// unrounded values), which stays inside the parity tolerance.
 constexpr int kMfmaTile = 32;   // tokens per wave iteration
 constexpr int kMfmaHeads = 16;  // query heads per workgroup (MFMA N)
 

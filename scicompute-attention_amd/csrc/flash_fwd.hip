@@ -7,21 +7,19 @@
 // q head h to kv head h / (H_q / H_kv), P is rounded to the input dtype before the PV product,
 // out = O / l (0 when l == 0), LSE = m + ln(l) (-inf when l == 0).
 //
-// MI355X design
-//   * workgroup = 4 waves = 128 query rows of one (batch, head); each wave owns 32 rows;
-//   * S^T = K Q^T with v_mfma_f32_32x32x16_{f16,bf16}: A = K rows from LDS (one 16 B read per
-//     lane), B = Q^T held in registers for the whole kernel. In the S^T accumulator every lane
-//     holds 16 keys of ONE query row, so the row max/sum need a single exchange between the two
-//     32-lane halves and the online-softmax state (m, l) is one register per lane;
-//   * the P^T accumulator registers, converted to fp16/bf16, are directly the B operand of
-//     O^T = V^T P^T (the key order inside an MFMA k-step is chosen to match the accumulator
-//     layout), so P never leaves registers;
-//   * V is transposed once per tile while it is staged into LDS (V^T rows = head-dim), so the
-//     A operand of the PV MFMA is two 8-byte LDS reads per lane;
-//   * K/V tiles are double-buffered in LDS with a register prefetch of the next tile issued
-//     before the current tile's MFMAs; one barrier per tile;
-//   * causal grids are issued longest-row-tile first (LPT order) and waves skip tiles that are
-//     fully masked for their 32 rows.
+// Two kernels share the formulation below:
+//   * flash_fwd_dma_kernel (head_dim 64 and 128, the serving shapes): K/V tiles DMA'd into LDS,
+//     8 waves per workgroup; described at its definition. It also serves packed variable-length
+//     batches in one launch (a device work list of (sequence, row tile), longest first);
+//   * flash_fwd_kernel (head_dim 32, 96, 160, 192, 256): 4 waves = 128 query rows, K/V staged
+//     through registers into a double-buffered LDS ring with V transposed on the way in.
+// Formulation: S^T = K Q^T with v_mfma_f32_32x32x16_{f16,bf16} (A = K rows from LDS, B = Q^T in
+// registers for the whole tile). In the S^T accumulator every lane holds 16 keys of ONE query
+// row, so the row max/sum need a single exchange between the two 32-lane halves and the
+// online-softmax state (m, l) is one register per lane. The P^T accumulator, converted to
+// fp16/bf16, is directly the B operand of O^T = V^T P^T (the key order inside an MFMA k-step
+// matches the accumulator layout), so P never leaves registers. The O rescale is lazy (only when
+// the running max grows by more than kRescaleSlack, decided per wave).
 
 #include <hip/hip_runtime.h>
 
@@ -442,19 +440,22 @@ __global__ __launch_bounds__(FlashGeom<D>::THREADS, 1) void flash_fwd_kernel(
 // ============================================================================================
 // DMA-pipelined variant for head_dim 64 and 128 (the serving shapes).
 //
-// K and V tiles go straight from global memory to LDS with global_load_lds_dwordx4 (no VGPR
-// staging, no transposition), through a 4-stage ring whose loads are issued two tiles ahead of
-// their use and retired with explicit vmcnt waits. LDS rows are unpadded; 16-byte chunks are
-// XOR-swizzled (K: chunk ^ (row % 8), V: chunk ^ 4*(row & 1)) so that both the K reads and the V
-// transpose reads are bank-conflict free. The PV A operand (V^T fragments) comes from
+// K and V tiles go straight from global memory to LDS with buffer loads to LDS (16 bytes per
+// lane, no VGPR staging, no transposition) through a buffer resource bounded at the sequence's
+// last row, so rows past seq_kv read as zero. Loads are issued ahead of their use and retired
+// with explicit vmcnt waits plus one barrier per tile. LDS rows are unpadded; 16-byte chunks are
+// XOR-swizzled per row (SwzK / SwzV) so that both the K reads and the V transpose reads are
+// bank-conflict free. The PV A operand (V^T fragments) comes from
 // ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j % 4 of the 8 bytes
 // read by lane 4*i + j/4 (i = 0..3), i.e. one head-dim column over 4 consecutive keys.
 // ============================================================================================
 // Two shapes, both 8 waves of 32 query rows x 32 keys per tile:
-//   RG = 4, KQ = 2: 128 query rows, 64-key tiles, a ring of 4 (K, V) stages (non-causal);
-//   RG = 2, KQ = 4: 64 query rows, 128-key tiles, two K slots + two V slots (causal: each
-//   workgroup runs the row tiles t and T-1-t one after the other, so every workgroup gets the
-//   same share of the triangle).
+//   RG = 4, KQ = 2: 128 query rows, 64-key tiles, a ring of 4 (K, V) stages (non-causal, large
+//   causal grids, varlen);
+//   RG = 2, KQ = 4: 64 query rows, 128-key tiles, three K slots + two V slots (small causal
+//   grids: each workgroup runs the row tiles T-1-t and t one after the other, so every
+//   workgroup gets the same share of the triangle).
+// The KQ waves of a row group split each key tile and are merged once, at the end, through LDS.
 template <int D, int RG, int KQ>
 struct DmaGeom {
     static_assert((RG == 4 && KQ == 2) || (RG == 2 && KQ == 4), "8 waves per workgroup");
