@@ -82,6 +82,19 @@ def time_launches(launch, steps, warmup):
     return start.elapsed_ms(stop) / steps
 
 
+def launch_percentiles(launch, runs=50):
+    """P50/P90/P99 of single launches (HIP events around each launch), in ms."""
+    events = [(H.Event(), H.Event()) for _ in range(runs)]
+    for a, b in events:
+        a.record()
+        launch()
+        b.record()
+    events[-1][1].synchronize()
+    ms = np.sort([a.elapsed_ms(b) for a, b in events])
+    return {"p50": float(np.percentile(ms, 50)), "p90": float(np.percentile(ms, 90)),
+            "p99": float(np.percentile(ms, 99))}
+
+
 # ---- C2: flash prefill -------------------------------------------------------------------------
 def bench_flash(steps, warmup, causal, B=1, Hh=8, S=4096, D=128):
     rng = np.random.default_rng(2024)
@@ -102,8 +115,9 @@ def bench_flash(steps, warmup, causal, B=1, Hh=8, S=4096, D=128):
     p.diagonal = 0
     ms = time_launches(lambda: H.flash_fwd(p), steps, warmup)
     flops = causal_flops(B, Hh, S, D) if causal else 4 * B * Hh * S * S * D
+    pct = launch_percentiles(lambda: H.flash_fwd(p))
     return {"ms": ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
-            "bytes": 4 * B * Hh * S * D * 2}
+            "bytes": 4 * B * Hh * S * D * 2, "pct": pct}
 
 
 # ---- C4: split-K decode --------------------------------------------------------------------------
@@ -311,10 +325,32 @@ def cpu_baseline(max_seconds=12.0):
             break
     secs = (time.perf_counter() - t0) / runs
     flops = causal_flops(1, 1, S, D)
+    # C1 (the reference's CPU configuration): B=1, H=8, D=64, S=128, fp32, non-causal; P50 of
+    # 100 runs after 20 warmup runs, on one thread and on all of them.
+    c1 = {}
+    S1, D1, H1 = 128, 64, 8
+    q1 = rng.standard_normal((1, H1, S1, D1), dtype=np.float32)
+    k1 = rng.standard_normal((1, H1, S1, D1), dtype=np.float32)
+    v1 = rng.standard_normal((1, H1, S1, D1), dtype=np.float32)
+    sc1 = np.empty(S1 * S1 * H1, np.float32)
+    o1 = np.empty_like(q1)
+    l1 = np.empty((1, H1, S1), np.float32)
+    scale1 = float(np.float32(1.0 / np.sqrt(D1)))
+    for nt in sorted({1, threads}):
+        times = []
+        for r in range(120):
+            t1 = time.perf_counter()
+            orc.naive_attention_into(q1, k1, v1, False, scale1, sc1, o1, l1, nt)
+            if r >= 20:
+                times.append(time.perf_counter() - t1)
+        p50 = float(np.percentile(times, 50))
+        c1[f"threads_{nt}"] = {"p50_ms": round(p50 * 1e3, 4),
+                               "gflops": round(4 * H1 * S1 * S1 * D1 / p50 / 1e9, 2)}
     return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"naive 3-pass FP32 restatement (attention_naive.cu:41-135) on one head of "
                       f"C2 (B=1,H=1,S=4096,D=128,causal), {runs} runs, {secs * 1e3:.1f} ms/run, "
-                      f"algorithmic causal FLOPs"}
+                      f"algorithmic causal FLOPs",
+            "c1": c1}
 
 
 def load_traffic(name):
@@ -386,7 +422,9 @@ def main():
         n = res["c2_noncausal"]
         line["prefill_noncausal"] = {"value": round(n["tflops"], 2), "unit": "TFLOP/s",
                                      "ms": round(n["ms"], 4),
-                                     "frac": round(n["tflops"] / PEAK_FP16_TFLOPS, 4)}
+                                     "frac": round(n["tflops"] / PEAK_FP16_TFLOPS, 4),
+                                     "launch_ms_pct": {k: round(v, 4) for k, v in n["pct"].items()}}
+        line["launch_ms_pct"] = {k: round(v, 4) for k, v in c["pct"].items()}
     if "c5_paged" in res:
         pg = res["c5_paged"]
         line["paged_decode"] = {
