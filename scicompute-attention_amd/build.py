@@ -128,6 +128,19 @@ def build_cpp_tests() -> str:
     return out
 
 
+def build_examples() -> list[str]:
+    """Example programs (examples/*.cpp), linked against libsca_host.so."""
+    outs = []
+    for src in sorted(glob.glob(os.path.join(PKG_DIR, "examples", "*.cpp"))):
+        out = os.path.join(LIB_DIR, os.path.splitext(os.path.basename(src))[0])
+        tmp = out + ".tmp"
+        _run([CXX, "-std=c++20", "-O2", "-Wall", "-I" + INCLUDE_DIR, src, "-o", tmp, "-L" + LIB_DIR,
+              "-lsca_host", "-lsca_hip", "-Wl,-rpath,$ORIGIN", "-pthread"])
+        os.replace(tmp, out)
+        outs.append(out)
+    return outs
+
+
 def build(workers: int | None = None) -> list[str]:
     workers = workers or min(8, os.cpu_count() or 4)
     if os.path.isdir(OBJ_DIR):
@@ -137,6 +150,7 @@ def build(workers: int | None = None) -> list[str]:
         outputs.append(build_host(workers))
         if os.path.exists(os.path.join(REPO_DIR, "tests", "cpp", "test_host_api.cpp")):
             outputs.append(build_cpp_tests())
+        outputs.extend(build_examples())
     return outputs
 
 
