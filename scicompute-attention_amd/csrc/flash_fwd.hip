@@ -590,7 +590,16 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     constexpr bool kPaired = kCausal && !kRing4;
     const int passes = kPaired ? ((2 * tile_linear + 1 < num_q_tiles) ? 2 : 1) : 1;
     // One row tile, start to finish (called once, or twice for a causal pair).
-    auto run_tile = [&](const int64_t qt) __attribute__((always_inline)) {
+    auto run_tile = [&](const int64_t qt_in) __attribute__((always_inline)) {
+    // The lane index and the tile go through an empty asm so that nothing of this tile's setup
+    // (DMA offsets, fragment addresses) is hoisted above the previous tile's epilogue, where it
+    // would only add register pressure.
+    int lane_v = lane;
+    int64_t qt = qt_in;
+    asm volatile("" : "+v"(lane_v), "+s"(qt));
+    const int lane = lane_v;
+    const int lr = lane & 31;
+    const int hh = lane >> 5;
     const int q0 = static_cast<int>(qt) * BM;
     const int wave_q0 = q0 + rg * kRowsPerWave;
     const int my_q = wave_q0 + lr;
@@ -914,21 +923,33 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
         }
         __syncthreads();
         if (kh == 0) {
+            // One maximum over the KQ states, then every O tile scaled and accumulated 16 values
+            // at a time (keeps the merge inside the register budget).
+            const float* mbuf0 = merge + ((0 * RG + rg) * kWave + lane) * G::MERGE_FLOATS;
+            constexpr int kStride = RG * kWave * G::MERGE_FLOATS;  // between the KQ-1 buffers
+            float mm = m_used;
+#pragma unroll
+            for (int q = 1; q < KQ; ++q) mm = fmaxf(mm, mbuf0[(q - 1) * kStride + G::DT * 16]);
+            float wq[KQ];
+            wq[0] = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
+            l_run *= wq[0];
 #pragma unroll
             for (int q = 1; q < KQ; ++q) {
-                const float* mbuf = merge + (((q - 1) * RG + rg) * kWave + lane) * G::MERGE_FLOATS;
-                const float m_o = mbuf[G::DT * 16];
-                const float l_o = mbuf[G::DT * 16 + 1];
-                const float mm = fmaxf(m_used, m_o);
-                const float wa = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
-                const float wb = (m_o == neg_inf()) ? 0.0f : fast_exp2(m_o - mm);
-                m_used = mm;
-                l_run = l_run * wa + l_o * wb;
+                const float m_o = mbuf0[(q - 1) * kStride + G::DT * 16];
+                wq[q] = (m_o == neg_inf()) ? 0.0f : fast_exp2(m_o - mm);
+                l_run += mbuf0[(q - 1) * kStride + G::DT * 16 + 1] * wq[q];
+            }
+            m_used = mm;
 #pragma unroll
-                for (int dt = 0; dt < G::DT; ++dt) {
+            for (int dt = 0; dt < G::DT; ++dt) {
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) o[dt][i] = o[dt][i] * wa + mbuf[dt * 16 + i] * wb;
+                for (int i = 0; i < 16; ++i) {
+                    float acc = o[dt][i] * wq[0];
+#pragma unroll
+                    for (int q = 1; q < KQ; ++q) acc += mbuf0[(q - 1) * kStride + dt * 16 + i] * wq[q];
+                    o[dt][i] = acc;
                 }
+                __builtin_amdgcn_sched_barrier(0);  // one O tile's LDS reads in flight at a time
             }
         }
     }
