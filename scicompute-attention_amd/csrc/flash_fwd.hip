@@ -940,6 +940,41 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
                 l_run += mbuf0[(q - 1) * kStride + G::DT * 16 + 1] * wq[q];
             }
             m_used = mm;
+            if constexpr (!kRing4) {
+                // Split layout: each O tile is merged and written out before the next one is
+                // touched (the paired passes leave no registers for a merged copy of O).
+                const float l_tot = HalfSum(l_run);
+                const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+                const bool row_ok = my_q < seq_q;
+                uint16_t* out_row = static_cast<uint16_t*>(p.out) + b * p.o_sb + h * p.o_sh +
+                                    (tok_q + my_q) * p.o_ss;
+#pragma unroll
+                for (int dt = 0; dt < G::DT; ++dt) {
+                    float acc[16];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        acc[i] = o[dt][i] * wq[0];
+#pragma unroll
+                        for (int q = 1; q < KQ; ++q) {
+                            acc[i] += mbuf0[(q - 1) * kStride + dt * 16 + i] * wq[q];
+                        }
+                    }
+                    if (row_ok) {
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            const int d0 = 32 * dt + 8 * g + 4 * hh;
+                            const uint32_t lo = M::pack(acc[4 * g + 0] * inv, acc[4 * g + 1] * inv);
+                            const uint32_t hi = M::pack(acc[4 * g + 2] * inv, acc[4 * g + 3] * inv);
+                            *reinterpret_cast<uint2*>(out_row + d0) = make_uint2(lo, hi);
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);  // one O tile in flight at a time
+                }
+                if (row_ok && p.lse != nullptr && hh == 0) {
+                    p.lse[(b * p.num_heads + h) * p.seq_q + my_q] =
+                        l_tot > 0.0f ? (m_used + __log2f(l_tot)) * kLn2 : neg_inf();
+                }
+            } else {
 #pragma unroll
             for (int dt = 0; dt < G::DT; ++dt) {
 #pragma unroll
@@ -951,9 +986,10 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
                 }
                 __builtin_amdgcn_sched_barrier(0);  // one O tile's LDS reads in flight at a time
             }
+            }
         }
     }
-    if (kh == 0) {
+    if (kRing4 && kh == 0) {
 
     const float l_tot = HalfSum(l_run);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
