@@ -560,8 +560,6 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int lane = tid % kWave;
-    const int lr = lane & 31;
-    const int hh = lane >> 5;
     const int rg = wave % RG;
     const int kh = wave / RG;
 
@@ -590,7 +588,27 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     constexpr bool kPaired = kCausal && !kRing4;
     const int passes = kPaired ? ((2 * tile_linear + 1 < num_q_tiles) ? 2 : 1) : 1;
     // One row tile, start to finish (called once, or twice for a causal pair).
-    auto run_tile = [&](const int64_t qt_in) __attribute__((always_inline)) {
+    // Query fragments of the current row tile (lane (lr, hh): row lr of the wave, k-step ks
+    // elements 16*ks + 8*hh .. +8; zero past seq_q).
+    vec8 qf[G::KS];
+    auto load_q = [&](const int64_t qt_l, const int lane_l) __attribute__((always_inline)) {
+        const int row = static_cast<int>(qt_l) * BM + rg * kRowsPerWave + (lane_l & 31);
+        const uint16_t* q_row = static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh +
+                                (tok_q + row) * p.q_ss + 8 * (lane_l >> 5);
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+            uint4 raw = make_uint4(0, 0, 0, 0);
+            if (row < wg_seq_q) raw = *reinterpret_cast<const uint4*>(q_row + 16 * ks);
+            qf[ks] = __builtin_bit_cast(vec8, raw);
+        }
+    };
+    // One row tile, start to finish. kOwnQ: the tile loads its own queries (else they were
+    // loaded by the previous tile); next_qt >= 0: the next tile's queries are loaded once this
+    // tile's DMAs have drained, so their latency hides behind the merge and the output stores.
+    // No wait follows a Q load: the Q loads are older than every tile DMA, so each vmcnt wait
+    // that retires a tile also retires them, and the first QK waits for them by itself.
+    auto run_tile = [&]<bool kOwnQ>(const int64_t qt_in, const int64_t next_qt)
+                        __attribute__((always_inline)) {
     // The lane index and the tile go through an empty asm so that nothing of this tile's setup
     // (DMA offsets, fragment addresses) is hoisted above the previous tile's epilogue, where it
     // would only add register pressure.
@@ -607,8 +625,6 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     const int seq_kv = wg_seq_kv;
     const int diag = wg_diag;
 
-    const uint16_t* q_ptr =
-        static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh + tok_q * p.q_ss;
     const uint8_t* k_bytes = reinterpret_cast<const uint8_t*>(
         static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh + tok_kv * p.k_ss);
     const uint8_t* v_bytes = reinterpret_cast<const uint8_t*>(
@@ -616,18 +632,7 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     const int k_row_bytes = static_cast<int>(p.k_ss) * 2;
     const int v_row_bytes = static_cast<int>(p.v_ss) * 2;
 
-    vec8 qf[G::KS];
-    {
-        const uint16_t* q_row = q_ptr + static_cast<int64_t>(my_q) * p.q_ss + 8 * hh;
-#pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks) {
-            uint4 raw = make_uint4(0, 0, 0, 0);
-            if (my_q < seq_q) raw = *reinterpret_cast<const uint4*>(q_row + 16 * ks);
-            qf[ks] = __builtin_bit_cast(vec8, raw);
-        }
-        // No wait here: the Q loads are older than every tile DMA, so each vmcnt wait below
-        // that retires a tile also retires them, and the first QK waits for them by itself.
-    }
+    if constexpr (kOwnQ) load_q(qt, lane);
 
     int n_tiles = (seq_kv + BN - 1) / BN;
     int n_plain = seq_kv / BN;
@@ -907,6 +912,7 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     // Drain the trailing DMAs before the LDS is reused for the merge (or released).
     WaitVm<0>();
     __builtin_amdgcn_s_barrier();
+    if (next_qt >= 0) load_q(next_qt, lane);
 
     // Merge the KQ key-slices of every row group into the kh == 0 wave.
     {
@@ -1015,15 +1021,17 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     };  // run_tile
 
     if constexpr (kPaired) {
-        run_tile(num_q_tiles - 1 - tile_linear);
+        run_tile.template operator()<true>(num_q_tiles - 1 - tile_linear,
+                                           passes == 2 ? tile_linear : -1);
         if (passes == 2) {
             __syncthreads();  // the first tile's merge buffer is the second tile's ring
-            run_tile(tile_linear);
+            run_tile.template operator()<false>(tile_linear, -1);
         }
     } else if constexpr (kVarlen) {
-        run_tile(var_qt);
+        run_tile.template operator()<true>(var_qt, -1);
     } else {
-        run_tile(kCausal ? num_q_tiles - 1 - tile_linear : tile_linear);
+        run_tile.template operator()<true>(kCausal ? num_q_tiles - 1 - tile_linear : tile_linear,
+                                           -1);
     }
 }
 
