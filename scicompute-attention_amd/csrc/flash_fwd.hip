@@ -464,21 +464,20 @@ struct DmaGeom {
     static constexpr int BM = RG * kRowsPerWave;  // query rows per workgroup
     static constexpr int WAVES = RG * KQ;
     static constexpr int THREADS = WAVES * kWave;
-    static constexpr int STAGES = kRing4 ? 4 : 2;
     // Split layout: K slots (3 when five tiles fit the 160 KB of LDS, so K is fetched two steps
     // ahead), then two V slots.
+    static constexpr int STAGES = kRing4 ? 4 : 2;  // tiles of K (and of V) the ring holds
     static constexpr int KSL = kRing4 ? 0 : (5 * BN * D * 2 <= 160 * 1024 ? 3 : 2);
     static constexpr int KS = D / 16;
     static constexpr int DT = D / 32;
     static constexpr int CPR = D / 8;             // 16-byte chunks per row
     static constexpr int TILE_BYTES = BN * D * 2; // one K or V tile
-    static constexpr int STAGE_BYTES = 2 * TILE_BYTES;
     static constexpr int IPW = BN * CPR / kWave / WAVES;  // DMA instructions per wave per tile
     static constexpr int LOADS_PER_TILE = 2 * IPW;        // K + V, per wave
     static constexpr int MERGE_FLOATS = DT * 16 + 2;
     static constexpr int MERGE_BYTES = RG * (KQ - 1) * kWave * MERGE_FLOATS * 4;
-    // kRing4: STAGES stages of (K tile, V tile). Otherwise KSL K tiles then two V tiles.
-    static constexpr int RING_BYTES = kRing4 ? STAGES * STAGE_BYTES : (KSL + 2) * TILE_BYTES;
+    // kRing4: four K slots then four V slots. Otherwise KSL K slots then two V slots.
+    static constexpr int RING_BYTES = (kRing4 ? 8 : KSL + 2) * TILE_BYTES;
     static constexpr int LDS_BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
     static_assert(IPW >= 1 && BN * CPR == IPW * kWave * WAVES, "tile must split evenly into DMAs");
 };
@@ -549,13 +548,11 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     constexpr int BN = G::BN;
     constexpr int ROW_BYTES = D * 2;
     constexpr int BM = G::BM;
-    static_assert(2 * G::STAGE_BYTES <= 65536 || !kRing4, "stage offsets must fit the 16-bit DS immediate");
-    static_assert(2 * G::TILE_BYTES <= 65536, "slot offsets must fit the 16-bit DS immediate");
+    // Slot offsets are DS immediates (the V ring's base lives in the per-lane offsets).
+    static_assert(kRing4 ? 3 * G::TILE_BYTES < 65536 : 2 * G::TILE_BYTES <= 65536,
+                  "slot offsets must fit the 16-bit DS immediate");
 
     extern __shared__ __align__(16) uint8_t lds8[];
-    // Stages 0/1 are addressed from lds8, stages 2/3 from lds8 + 2 stages; within each half the
-    // stage offset is a DS immediate.
-    uint8_t* const lds_hi = lds8 + 2 * G::STAGE_BYTES;
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -663,13 +660,12 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
         dma_voff[i] = row * v_row_bytes + (pos ^ SwzV<D>(row)) * 16;
     }
 
-    // LDS homes of tile t's K and V: RG = 4, stage S = t & 3 holds (K, V); RG = 2, K slot t & 1
-    // and V slot t & 1 (K tiles first, then V tiles).
+    // LDS homes of tile t's K and V: K slots first (RG = 4: four, slot t & 3; RG = 2: KSL, slot
+    // t % KSL), then the V slots (RG = 4: four, slot t & 3; RG = 2: two, slot t & 1).
     auto v_home = [&]<int S>() -> uint8_t* {
-        return kRing4 ? lds8 + S * G::STAGE_BYTES + G::TILE_BYTES
-                      : lds8 + (G::KSL + S) * G::TILE_BYTES;
+        return lds8 + ((kRing4 ? 4 : G::KSL) + S) * G::TILE_BYTES;
     };
-    // Split layout: K tile t goes to K slot `slot` (= t % KSL, tracked by the caller).
+    // K tile t goes to K slot `slot` (tracked by the caller).
     auto issue_k = [&](int slot, int t) {
         uint8_t* k_dst = lds8 + slot * G::TILE_BYTES + wave * G::IPW * 1024;
         const uint32_t k_tile_off = static_cast<uint32_t>(t * BN * k_row_bytes);
@@ -686,21 +682,6 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
             DmaToLds(v_bytes, v_records, v_dst + i * 1024, dma_voff[i], v_tile_off);
         }
     };
-    auto issue_tile = [&]<int S>(int t) {
-        uint8_t* k_dst = lds8 + S * G::STAGE_BYTES + wave * G::IPW * 1024;
-        uint8_t* v_dst = k_dst + G::TILE_BYTES;
-        const uint32_t k_tile_off = static_cast<uint32_t>(t * BN * k_row_bytes);
-        const uint32_t v_tile_off = static_cast<uint32_t>(t * BN * v_row_bytes);
-#pragma unroll
-        for (int i = 0; i < G::IPW; ++i) {
-            DmaToLds(k_bytes, k_records, k_dst + i * 1024, dma_koff[i], k_tile_off);
-        }
-#pragma unroll
-        for (int i = 0; i < G::IPW; ++i) {
-            DmaToLds(v_bytes, v_records, v_dst + i * 1024, dma_voff[i], v_tile_off);
-        }
-    };
-
     floatx16 o[G::DT];
 #pragma unroll
     for (int dt = 0; dt < G::DT; ++dt) {
@@ -732,7 +713,7 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     for (int dt = 0; dt < G::DT; ++dt) {
         // The V slots of the split layout start 2 tiles in; that base lives in the per-lane
         // offset so the slot offset stays a DS immediate.
-        v_frag[dt] = (kRing4 ? 0 : G::KSL * G::TILE_BYTES) + v_key * ROW_BYTES +
+        v_frag[dt] = (kRing4 ? 4 : G::KSL) * G::TILE_BYTES + v_key * ROW_BYTES +
                      (((4 * dt + v_chunk) ^ SwzV<D>(v_key)) * 16) + v_half;
     }
 
@@ -747,14 +728,40 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
         for (int ks = 0; ks < G::KS; ++ks) acc = M::mma(a[ks], qf[ks], acc);
         return acc;
     };
-    auto qk = [&]<int S>() {
-        return qk_at((S < 2 ? lds8 : lds_hi) + (S & 1) * G::STAGE_BYTES);
-    };
     auto qk_slot = [&](int slot) { return qk_at(lds8 + slot * G::TILE_BYTES); };
 
-    // One pipeline step for tile j (held in stage S; tile j+1 in stage S+1, tiles j+2 and j+3
-    // in flight): QK MFMAs of tile j+1 interleaved with the softmax VALU of tile j, the O rescale
-    // when some lane's running max moved, PV MFMAs of tile j, then retire tile j+2 and sync.
+    // P V^T for one key tile: V^T fragments from the V tile at vbase, P from pw (8 packed pairs).
+    auto pv_at = [&](const uint8_t* vbase, const uint32_t (&pw)[8]) {
+        const vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+        const vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
+        vec8 va[G::DT][2];
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+            for (int ps = 0; ps < 2; ++ps) {
+                const uint2 lo = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps) * ROW_BYTES);
+                const uint2 hi = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps + 8) * ROW_BYTES);
+                va[dt][ps] = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+            o[dt] = M::mma(va[dt][0], pb0, o[dt]);
+            o[dt] = M::mma(va[dt][1], pb1, o[dt]);
+        }
+        // V^T fragments for two O tiles at a time ahead of their MFMAs
+#pragma unroll
+        for (int dt = 0; dt < G::DT; dt += 2) {
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+        }
+    };
+
+    // One pipeline step for tile j: QK MFMAs of tile j+1 interleaved with the softmax VALU of
+    // tile j, the O rescale when some lane's running max moved, then PV of tile j; then retire
+    // the tiles the next step needs and sync.
+    // RG = 4 (S = j & 3; K slots and V slots are rings of four): the step issues K(j+3) into the
+    // slot K(j-1) left and V(j+2) into the slot V(j-2) left; K(j+2) and V(j+1) land by its end.
     // Split layout (S = j & 1): V of tile j+1 goes to the slot V(j-1) left and K of tile
     // j+KSL to the slot K(j) left (read by the previous step's QK). V(j+1) and K(j+2) must land
     // by the end of this step; with three K slots K(j+3) may stay in flight.
@@ -762,8 +769,9 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     // (`masked` is uniform; kMaskable = false compiles the plain step).
     auto step = [&]<bool kMaskable, int S>(int j, floatx16& s_in, floatx16& s_out, bool masked) {
         if constexpr (kRing4) {
-            issue_tile.template operator()<(S + 3) & 3>(j + 3);
-            s_out = qk.template operator()<(S + 1) & 3>();
+            issue_k((S + 3) & 3, j + 3);
+            issue_v.template operator()<(S + 2) & 3>(j + 2);
+            s_out = qk_slot((S + 1) & 3);
         } else {
             issue_v.template operator()<S ^ 1>(j + 1);
             issue_k(j % G::KSL, j + G::KSL);
@@ -817,37 +825,10 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
             }
         }
 
-        const vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-        const vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
-        const uint8_t* vbase = kRing4
-                                   ? (S < 2 ? lds8 : lds_hi) + (S & 1) * G::STAGE_BYTES + G::TILE_BYTES
-                                   : lds8 + S * G::TILE_BYTES;
-        vec8 va[G::DT][2];
-#pragma unroll
-        for (int dt = 0; dt < G::DT; ++dt) {
-#pragma unroll
-            for (int ps = 0; ps < 2; ++ps) {
-                const uint2 lo = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps) * ROW_BYTES);
-                const uint2 hi = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps + 8) * ROW_BYTES);
-                va[dt][ps] = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-            }
-        }
-#pragma unroll
-        for (int dt = 0; dt < G::DT; ++dt) {
-            o[dt] = M::mma(va[dt][0], pb0, o[dt]);
-            o[dt] = M::mma(va[dt][1], pb1, o[dt]);
-        }
+        pv_at(lds8 + S * G::TILE_BYTES, pw);
 
-        // V^T fragments for two O tiles at a time ahead of their MFMAs
-#pragma unroll
-        for (int dt = 0; dt < G::DT; dt += 2) {
-            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
-        }
-
-        // RG = 4: tile j+2 has landed (tile j+3 may still be in flight). RG = 2: K(j+2) and
-        // V(j+1) have landed. Publish them, and make sure every wave is done with the LDS this
-        // step read before the next step refills it.
+        // Publish the tiles that landed, and make sure every wave is done with the LDS this step
+        // read before the next step refills it.
         if constexpr (kRing4) {
             WaitVm<G::LOADS_PER_TILE>();
         } else if constexpr (G::KSL == 3) {
@@ -859,16 +840,17 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
         __builtin_amdgcn_s_barrier();
     };
 
-    floatx16 s0, s1;
-    int j = 0;
     if constexpr (kRing4) {
-        issue_tile.template operator()<0>(0);
-        issue_tile.template operator()<1>(1);
-        issue_tile.template operator()<2>(2);
-        WaitVm<G::LOADS_PER_TILE>();  // tiles 0 and 1 landed (tile 2 may be in flight)
+        issue_k(0, 0);
+        issue_k(1, 1);
+        issue_v.template operator()<0>(0);
+        issue_k(2, 2);
+        issue_v.template operator()<1>(1);
+        WaitVm<G::LOADS_PER_TILE>();  // K(0), K(1), V(0) landed (K(2), V(1) may be in flight)
         __builtin_amdgcn_s_barrier();
-        s0 = qk.template operator()<0>();
-        // Steady state: four steps per trip, stages fixed at compile time, scores ping-pong.
+        floatx16 s0 = qk_slot(0), s1;
+        int j = 0;
+        // Steady state: four steps per trip, slots fixed at compile time, scores ping-pong.
         for (; j + 4 <= n_plain; j += 4) {
             step.template operator()<false, 0>(j, s0, s1, false);
             step.template operator()<false, 1>(j + 1, s1, s0, false);
@@ -886,6 +868,8 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
             s0 = s1;
         }
     } else {
+        floatx16 s0, s1;
+        int j = 0;
         issue_k(0, 0);
         issue_k(1, 1);
         issue_v.template operator()<0>(0);
