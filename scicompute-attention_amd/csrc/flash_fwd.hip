@@ -768,13 +768,17 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     // kMaskable && masked: the tile reaches past the causal diagonal or the end of the keys
     // (`masked` is uniform; kMaskable = false compiles the plain step).
     auto step = [&]<bool kMaskable, int S>(int j, floatx16& s_in, floatx16& s_out, bool masked) {
+        // Tiles past the last one are not fetched (uniform; the plain steps of the ring loop are
+        // never that close to the end).
+        const bool more_k = !kMaskable || j + (kRing4 ? 3 : G::KSL) < n_tiles;
+        const bool more_v = !kMaskable || j + (kRing4 ? 2 : 1) < n_tiles;
         if constexpr (kRing4) {
-            issue_k((S + 3) & 3, j + 3);
-            issue_v.template operator()<(S + 2) & 3>(j + 2);
+            if (more_k) issue_k((S + 3) & 3, j + 3);
+            if (more_v) issue_v.template operator()<(S + 2) & 3>(j + 2);
             s_out = qk_slot((S + 1) & 3);
         } else {
-            issue_v.template operator()<S ^ 1>(j + 1);
-            issue_k(j % G::KSL, j + G::KSL);
+            if (more_v) issue_v.template operator()<S ^ 1>(j + 1);
+            if (more_k) issue_k(j % G::KSL, j + G::KSL);
             s_out = qk_slot((j + 1) % G::KSL);
         }
         floatx16 sv = s_in;
@@ -829,10 +833,22 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
 
         // Publish the tiles that landed, and make sure every wave is done with the LDS this step
         // read before the next step refills it.
+        // The DMAs this step issued may stay in flight (in the split layout with three K slots,
+        // only K(j+3)).
         if constexpr (kRing4) {
-            WaitVm<G::LOADS_PER_TILE>();
+            if (more_k) {
+                WaitVm<G::LOADS_PER_TILE>();
+            } else if (more_v) {
+                WaitVm<G::IPW>();
+            } else {
+                WaitVm<0>();
+            }
         } else if constexpr (G::KSL == 3) {
-            WaitVm<G::IPW>();
+            if (more_k) {
+                WaitVm<G::IPW>();
+            } else {
+                WaitVm<0>();
+            }
         } else {
             WaitVm<0>();
         }
@@ -898,36 +914,43 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     __builtin_amdgcn_s_barrier();
     if (next_qt >= 0) load_q(next_qt, lane);
 
-    // Merge the KQ key-slices of every row group into the kh == 0 wave.
+    // Merge the KQ key-slices of every row group into the kh == 0 wave. Buffer of wave (kh, rg):
+    // O as 16-byte quads, quad k of lane L at ((kh-1)*RG + rg) * 4*DT*64 + k*64 + L (lane-major,
+    // so every access is a conflict-free 16-byte one), then (m, l) pairs at the end.
     {
-        float* const merge = reinterpret_cast<float*>(lds8);
+        float4* const mquad = reinterpret_cast<float4*>(lds8);
+        float2* const mstat = reinterpret_cast<float2*>(mquad + (KQ - 1) * RG * 4 * G::DT * kWave);
         if (kh != 0) {
-            float* mbuf = merge + (((kh - 1) * RG + rg) * kWave + lane) * G::MERGE_FLOATS;
+            float4* mbuf = mquad + ((kh - 1) * RG + rg) * 4 * G::DT * kWave + lane;
 #pragma unroll
             for (int dt = 0; dt < G::DT; ++dt) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) mbuf[dt * 16 + i] = o[dt][i];
+                for (int g = 0; g < 4; ++g) {
+                    mbuf[(4 * dt + g) * kWave] = make_float4(o[dt][4 * g], o[dt][4 * g + 1],
+                                                             o[dt][4 * g + 2], o[dt][4 * g + 3]);
+                }
             }
-            mbuf[G::DT * 16] = m_used;
-            mbuf[G::DT * 16 + 1] = l_run;
+            mstat[((kh - 1) * RG + rg) * kWave + lane] = make_float2(m_used, l_run);
         }
         __syncthreads();
         if (kh == 0) {
             // One maximum over the KQ states, then every O tile scaled and accumulated 16 values
             // at a time (keeps the merge inside the register budget).
-            const float* mbuf0 = merge + ((0 * RG + rg) * kWave + lane) * G::MERGE_FLOATS;
-            constexpr int kStride = RG * kWave * G::MERGE_FLOATS;  // between the KQ-1 buffers
+            const float4* mbuf0 = mquad + rg * 4 * G::DT * kWave + lane;
+            constexpr int kStride = RG * 4 * G::DT * kWave;  // quads between the KQ-1 buffers
+            float2 st[KQ];
+#pragma unroll
+            for (int q = 1; q < KQ; ++q) st[q] = mstat[((q - 1) * RG + rg) * kWave + lane];
             float mm = m_used;
 #pragma unroll
-            for (int q = 1; q < KQ; ++q) mm = fmaxf(mm, mbuf0[(q - 1) * kStride + G::DT * 16]);
+            for (int q = 1; q < KQ; ++q) mm = fmaxf(mm, st[q].x);
             float wq[KQ];
             wq[0] = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
             l_run *= wq[0];
 #pragma unroll
             for (int q = 1; q < KQ; ++q) {
-                const float m_o = mbuf0[(q - 1) * kStride + G::DT * 16];
-                wq[q] = (m_o == neg_inf()) ? 0.0f : fast_exp2(m_o - mm);
-                l_run += mbuf0[(q - 1) * kStride + G::DT * 16 + 1] * wq[q];
+                wq[q] = (st[q].x == neg_inf()) ? 0.0f : fast_exp2(st[q].x - mm);
+                l_run += st[q].y * wq[q];
             }
             m_used = mm;
             if constexpr (!kRing4) {
@@ -942,11 +965,16 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
                 for (int dt = 0; dt < G::DT; ++dt) {
                     float acc[16];
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        acc[i] = o[dt][i] * wq[0];
+                    for (int i = 0; i < 16; ++i) acc[i] = o[dt][i] * wq[0];
 #pragma unroll
-                        for (int q = 1; q < KQ; ++q) {
-                            acc[i] += mbuf0[(q - 1) * kStride + dt * 16 + i] * wq[q];
+                    for (int q = 1; q < KQ; ++q) {
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            const float4 v = mbuf0[(q - 1) * kStride + (4 * dt + g) * kWave];
+                            acc[4 * g] += v.x * wq[q];
+                            acc[4 * g + 1] += v.y * wq[q];
+                            acc[4 * g + 2] += v.z * wq[q];
+                            acc[4 * g + 3] += v.w * wq[q];
                         }
                     }
                     if (row_ok) {
@@ -958,7 +986,6 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
                             *reinterpret_cast<uint2*>(out_row + d0) = make_uint2(lo, hi);
                         }
                     }
-                    __builtin_amdgcn_sched_barrier(0);  // one O tile in flight at a time
                 }
                 if (row_ok && p.lse != nullptr && hh == 0) {
                     p.lse[(b * p.num_heads + h) * p.seq_q + my_q] =
@@ -968,11 +995,17 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
 #pragma unroll
             for (int dt = 0; dt < G::DT; ++dt) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    float acc = o[dt][i] * wq[0];
+                for (int i = 0; i < 16; ++i) o[dt][i] *= wq[0];
 #pragma unroll
-                    for (int q = 1; q < KQ; ++q) acc += mbuf0[(q - 1) * kStride + dt * 16 + i] * wq[q];
-                    o[dt][i] = acc;
+                for (int q = 1; q < KQ; ++q) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const float4 v = mbuf0[(q - 1) * kStride + (4 * dt + g) * kWave];
+                        o[dt][4 * g] += v.x * wq[q];
+                        o[dt][4 * g + 1] += v.y * wq[q];
+                        o[dt][4 * g + 2] += v.z * wq[q];
+                        o[dt][4 * g + 3] += v.w * wq[q];
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);  // one O tile's LDS reads in flight at a time
             }
