@@ -760,8 +760,10 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     // One pipeline step for tile j: QK MFMAs of tile j+1 interleaved with the softmax VALU of
     // tile j, the O rescale when some lane's running max moved, then PV of tile j; then retire
     // the tiles the next step needs and sync.
-    // RG = 4 (S = j & 3; K slots and V slots are rings of four): the step issues K(j+3) into the
-    // slot K(j-1) left and V(j+2) into the slot V(j-2) left; K(j+2) and V(j+1) land by its end.
+    // RG = 4 (S = j & 3; K slots and V slots are rings of four): steps go in pairs with one
+    // barrier per pair. The even step issues K(j+3), K(j+4) into the slots K(j-1), K(j) left and
+    // V(j+2), V(j+3) into the slots V(j-2), V(j-1) left (all read before the previous pair's
+    // barrier); the odd step retires them and syncs.
     // Split layout (S = j & 1): V of tile j+1 goes to the slot V(j-1) left and K of tile
     // j+KSL to the slot K(j) left (read by the previous step's QK). V(j+1) and K(j+2) must land
     // by the end of this step; with three K slots K(j+3) may stay in flight.
@@ -770,11 +772,15 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     auto step = [&]<bool kMaskable, int S>(int j, floatx16& s_in, floatx16& s_out, bool masked) {
         // Tiles past the last one are not fetched (uniform; the plain steps of the ring loop are
         // never that close to the end).
-        const bool more_k = !kMaskable || j + (kRing4 ? 3 : G::KSL) < n_tiles;
-        const bool more_v = !kMaskable || j + (kRing4 ? 2 : 1) < n_tiles;
+        const bool more_k = !kMaskable || j + G::KSL < n_tiles;  // split layout
+        const bool more_v = !kMaskable || j + 1 < n_tiles;
         if constexpr (kRing4) {
-            if (more_k) issue_k((S + 3) & 3, j + 3);
-            if (more_v) issue_v.template operator()<(S + 2) & 3>(j + 2);
+            if constexpr ((S & 1) == 0) {
+                if (!kMaskable || j + 3 < n_tiles) issue_k((S + 3) & 3, j + 3);
+                if (!kMaskable || j + 4 < n_tiles) issue_k(S, j + 4);
+                if (!kMaskable || j + 2 < n_tiles) issue_v.template operator()<(S + 2) & 3>(j + 2);
+                if (!kMaskable || j + 3 < n_tiles) issue_v.template operator()<(S + 3) & 3>(j + 3);
+            }
             s_out = qk_slot((S + 1) & 3);
         } else {
             if (more_v) issue_v.template operator()<S ^ 1>(j + 1);
@@ -833,16 +839,11 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
 
         // Publish the tiles that landed, and make sure every wave is done with the LDS this step
         // read before the next step refills it.
-        // The DMAs this step issued may stay in flight (in the split layout with three K slots,
-        // only K(j+3)).
+        // RG = 4: the odd step of a pair retires the pair's DMAs. Split layout: the DMAs this
+        // step issued may stay in flight (with three K slots, only K(j+3)).
         if constexpr (kRing4) {
-            if (more_k) {
-                WaitVm<G::LOADS_PER_TILE>();
-            } else if (more_v) {
-                WaitVm<G::IPW>();
-            } else {
-                WaitVm<0>();
-            }
+            if constexpr ((S & 1) == 0) return;
+            WaitVm<0>();
         } else if constexpr (G::KSL == 3) {
             if (more_k) {
                 WaitVm<G::IPW>();
@@ -862,7 +863,7 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
         issue_v.template operator()<0>(0);
         issue_k(2, 2);
         issue_v.template operator()<1>(1);
-        WaitVm<G::LOADS_PER_TILE>();  // K(0), K(1), V(0) landed (K(2), V(1) may be in flight)
+        WaitVm<0>();
         __builtin_amdgcn_s_barrier();
         floatx16 s0 = qk_slot(0), s1;
         int j = 0;
