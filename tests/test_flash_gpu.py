@@ -50,6 +50,15 @@ def test_non_tile_multiples(hip, seq):
         _case("f16", causal, 1, 8, 8, seq, seq, 128, 30000 + 2 * seq + j)
 
 
+@pytest.mark.parametrize("skv", [192, 256, 257, 320, 448, 449])
+def test_key_tile_counts(hip, skv):
+    # 3 to 8 key tiles of 64: every parity of the last step within the paired-barrier steps of
+    # the 128-row kernel, with and without a partial tail tile; causal is bottom-right aligned
+    for j, causal in enumerate([False, True]):
+        _case("bf16", causal, 1, 4, 2, 96, skv, 128, 31000 + 2 * skv + j)
+        _case("f16", causal, 1, 4, 4, 64, skv, 64, 32000 + 2 * skv + j)
+
+
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
 def test_gqa_groups(hip, group):
     _case("f16", True, 2, 8 * group, 8, 96, 160, 128, 40000 + group)
