@@ -450,8 +450,8 @@ __global__ __launch_bounds__(FlashGeom<D>::THREADS, 1) void flash_fwd_kernel(
 // read by lane 4*i + j/4 (i = 0..3), i.e. one head-dim column over 4 consecutive keys.
 // ============================================================================================
 // Two shapes, both 8 waves of 32 query rows x 32 keys per tile:
-//   RG = 4, KQ = 2: 128 query rows, 64-key tiles, a ring of 4 (K, V) stages (non-causal, large
-//   causal grids, varlen);
+//   RG = 4, KQ = 2: 128 query rows, 64-key tiles, rings of four K slots and four V slots, one
+//   barrier per pair of tiles (non-causal, large causal grids, varlen);
 //   RG = 2, KQ = 4: 64 query rows, 128-key tiles, three K slots + two V slots (small causal
 //   grids: each workgroup runs the row tiles T-1-t and t one after the other, so every
 //   workgroup gets the same share of the triangle).
