@@ -866,6 +866,9 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
         WaitVm<0>();
         __builtin_amdgcn_s_barrier();
         floatx16 s0 = qk_slot(0), s1;
+        // Every wave has read K(0) before step 0 refills its slot with K(4).
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
         int j = 0;
         // Steady state: four steps per trip, slots fixed at compile time, scores ping-pong.
         for (; j + 4 <= n_plain; j += 4) {
