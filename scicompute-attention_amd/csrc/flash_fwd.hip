@@ -863,10 +863,12 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
         issue_v.template operator()<0>(0);
         issue_k(2, 2);
         issue_v.template operator()<1>(1);
-        WaitVm<0>();
+        WaitVm<4 * G::IPW>();  // K(0) landed; the first QK runs while the rest arrive
         __builtin_amdgcn_s_barrier();
         floatx16 s0 = qk_slot(0), s1;
-        // Every wave has read K(0) before step 0 refills its slot with K(4).
+        // Every wave has read K(0) before step 0 refills its slot with K(4); K(1), V(0), K(2),
+        // V(1) are published by the same barrier.
+        WaitVm<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
         int j = 0;
@@ -895,13 +897,19 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
         issue_v.template operator()<0>(0);
         if constexpr (G::KSL == 3) {
             issue_k(2, 2);
-            WaitVm<G::IPW>();  // K(0), K(1), V(0) landed (K(2) may be in flight)
+            WaitVm<3 * G::IPW>();  // K(0) landed; the first QK runs while the rest arrive
         } else {
-            WaitVm<0>();
+            WaitVm<2 * G::IPW>();
         }
         __builtin_amdgcn_s_barrier();
         s0 = qk_slot(0);
-        // Every wave has read K(0) before step 0 refills its slot.
+        // Every wave has read K(0) before step 0 refills its slot; K(1) and V(0) are published
+        // by the same barrier (K(2) may stay in flight).
+        if constexpr (G::KSL == 3) {
+            WaitVm<G::IPW>();
+        } else {
+            WaitVm<0>();
+        }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
         // Two steps per trip (stages fixed at compile time); tiles from n_plain on are masked
