@@ -49,12 +49,12 @@ def f16_bits(rng, shape):
     return rng.standard_normal(size=shape, dtype=np.float32).astype(np.float16).view(np.uint16)
 
 
-def bf16_bits(rng, shape, chunk=1 << 24):
-    """Seeded N(0,1) bf16 bits; large tensors tile one random chunk (the values do not change
-    the amount of work)."""
+def bf16_bits(rng, shape, chunk=1 << 24, std=1.0):
+    """Seeded N(0, std^2) bf16 bits; large tensors tile one random chunk (the values do not
+    change the amount of work)."""
     n = int(np.prod(shape))
     m = min(n, chunk)
-    x = rng.standard_normal(size=m, dtype=np.float32).view(np.uint32)
+    x = (rng.standard_normal(size=m, dtype=np.float32) * np.float32(std)).view(np.uint32)
     bits = ((x + 0x7FFF + ((x >> 16) & 1)) >> 16).astype(np.uint16)
     if m < n:
         bits = np.resize(bits, n)
@@ -118,6 +118,30 @@ def bench_flash(steps, warmup, causal, B=1, Hh=8, S=4096, D=128):
     pct = launch_percentiles(lambda: H.flash_fwd(p))
     return {"ms": ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
             "bytes": 4 * B * Hh * S * D * 2, "pct": pct}
+
+
+# ---- C3: GQA causal prefill (reported next to the headline) -----------------------------------
+def bench_flash_gqa(steps, warmup, B=4, Hq=32, Hkv=8, S=8192, D=128):
+    """C3: bf16 Q/K/V ~ N(0, 0.5^2), causal, group 4; flash through the C ABI."""
+    rng = np.random.default_rng(2025)
+    dq = H.DeviceBuffer.from_array(bf16_bits(rng, (B, Hq, S, D), std=0.5))
+    dk = H.DeviceBuffer.from_array(bf16_bits(rng, (B, Hkv, S, D), std=0.5))
+    dv = H.DeviceBuffer.from_array(bf16_bits(rng, (B, Hkv, S, D), std=0.5))
+    dout = H.DeviceBuffer(B * Hq * S * D * 2)
+    p = H.FlashParams()
+    p.q, p.k, p.v, p.out, p.lse = dq.ptr, dk.ptr, dv.ptr, dout.ptr, None
+    p.batch, p.num_heads, p.num_kv_heads, p.seq_q, p.seq_kv, p.head_dim = B, Hq, Hkv, S, S, D
+    p.q_sb, p.q_sh, p.q_ss = Hq * S * D, S * D, D
+    p.k_sb, p.k_sh, p.k_ss = Hkv * S * D, S * D, D
+    p.v_sb, p.v_sh, p.v_ss = p.k_sb, p.k_sh, p.k_ss
+    p.o_sb, p.o_sh, p.o_ss = p.q_sb, p.q_sh, p.q_ss
+    p.scale = float(np.float32(1.0 / np.sqrt(D)))
+    p.causal = 1
+    p.dtype = H.DTYPE_BF16
+    p.diagonal = 0
+    ms = time_launches(lambda: H.flash_fwd(p), steps, warmup)
+    flops = causal_flops(B, Hq, S, D)
+    return {"ms": ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
 # ---- C4: split-K decode --------------------------------------------------------------------------
@@ -370,12 +394,12 @@ def main():
     ap.add_argument("--paged-steps", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="all",
-                    help="comma list of prefill, paged, paged_host, decode, copy "
+                    help="comma list of prefill, gqa, paged, paged_host, decode, copy "
                          "(default: all but copy)")
     args = ap.parse_args()
-    parts = ({"prefill", "paged", "paged_host", "decode"} if args.only == "all"
+    parts = ({"prefill", "gqa", "paged", "paged_host", "decode"} if args.only == "all"
              else set(args.only.split(",")))
-    unknown = parts - {"prefill", "paged", "paged_host", "decode", "copy"}
+    unknown = parts - {"prefill", "gqa", "paged", "paged_host", "decode", "copy"}
     if unknown:
         ap.error(f"unknown --only part(s): {sorted(unknown)}")
     if args.gpus != 1:
@@ -391,6 +415,8 @@ def main():
     if "prefill" in parts:
         res["c2_causal"] = bench_flash(args.steps, args.warmup, True)
         res["c2_noncausal"] = bench_flash(args.steps, args.warmup, False)
+    if "gqa" in parts:
+        res["c3_gqa"] = bench_flash_gqa(max(5, args.steps // 5), 3)
     if "paged" in parts:
         res["c5_paged"] = bench_paged(args.paged_steps)
     if "paged_host" in parts:
@@ -425,6 +451,13 @@ def main():
                                      "frac": round(n["tflops"] / PEAK_FP16_TFLOPS, 4),
                                      "launch_ms_pct": {k: round(v, 4) for k, v in n["pct"].items()}}
         line["launch_ms_pct"] = {k: round(v, 4) for k, v in c["pct"].items()}
+    if "c3_gqa" in res:
+        g = res["c3_gqa"]
+        line["gqa_prefill_c3"] = {
+            "value": round(g["tflops"], 2), "unit": "TFLOP/s", "dtype": "bf16",
+            "ms": round(g["ms"], 4), "frac": round(g["tflops"] / PEAK_FP16_TFLOPS, 4),
+            "workload": "C3 GQA causal flash prefill bf16 B=4 Hq=32 Hkv=8 D=128 S=8192, "
+                        "N(0, 0.5^2)"}
     if "c5_paged" in res:
         pg = res["c5_paged"]
         line["paged_decode"] = {
