@@ -7,10 +7,13 @@
 // q head h to kv head h / (H_q / H_kv), P is rounded to the input dtype before the PV product,
 // out = O / l (0 when l == 0), LSE = m + ln(l) (-inf when l == 0).
 //
-// Two kernels share the formulation below:
+// Three kernels share the formulation below:
 //   * flash_fwd_dma_kernel (head_dim 64 and 128, the serving shapes): K/V tiles DMA'd into LDS,
 //     8 waves per workgroup; described at its definition. It also serves packed variable-length
 //     batches in one launch (a device work list of (sequence, row tile), longest first);
+//   * flash_fwd_pair_kernel (head_dim 64 and 128, causal grids too small to balance 128-row
+//     tiles): the same DMA pipeline in two 4-wave groups that run a complementary pair of
+//     64-row tiles side by side; described at its definition;
 //   * flash_fwd_kernel (head_dim 32, 96, 160, 192, 256): 4 waves = 128 query rows, K/V staged
 //     through registers into a double-buffered LDS ring with V transposed on the way in.
 // Formulation: S^T = K Q^T with v_mfma_f32_32x32x16_{f16,bf16} (A = K rows from LDS, B = Q^T in
@@ -1064,6 +1067,458 @@ __global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dm
     }
 }
 
+// ---- Two-group causal pair kernel ---------------------------------------------------------------
+// Small causal grids: each workgroup owns the complementary 64-row tiles A = T-1-t (long) and
+// B = t (short) and runs them concurrently in two groups of four waves (one wave of each group
+// per SIMD), each group with its own K/V ring. Group 0 takes A's key tiles [0, x); group 1
+// takes all of B, finishes B (a two-way merge and the stores), then takes A's key tiles
+// [x, n_A). The two groups' A states are merged once at the end, so the short tile's setup,
+// merge and stores run beside the long tile's key loop instead of after it. x balances the
+// two groups' barrier intervals.
+// Within a group: 2 row groups of 32 rows x 2 waves of 32 keys per 64-key tile; the pipeline
+// step j computes QK of tile j+1 under the softmax of tile j, then PV of tile j.
+template <int D>
+struct PairGeom {
+    static constexpr int GW = 4;                      // waves per group
+    static constexpr int THREADS = 2 * GW * kWave;
+    static constexpr int BM = 64;                     // rows per row tile
+    static constexpr int BN = 64;                     // keys per key tile
+    static constexpr int KS = D / 16;
+    static constexpr int DT = D / 32;
+    static constexpr int CPR = D / 8;
+    static constexpr int ROW_BYTES = D * 2;
+    static constexpr int TILE_BYTES = BN * D * 2;
+    static constexpr int IPW = BN * CPR / (kWave * GW);  // DMA instructions per wave per tile
+    static constexpr int RING_BYTES = 4 * TILE_BYTES;    // K slots 0, 1, then V slots 0, 1
+    static constexpr int MERGE_FLOATS = DT * 16 + 2;
+    // Final merge: per row group, three partial states (16-byte quads) and their (m, l).
+    static constexpr int MERGE_QUADS = 2 * 3 * 4 * DT * kWave;
+    static constexpr int MERGE_BYTES = MERGE_QUADS * 16 + 2 * 3 * kWave * 8;
+    static constexpr int LDS_BYTES = 2 * RING_BYTES > MERGE_BYTES ? 2 * RING_BYTES : MERGE_BYTES;
+    static_assert(IPW >= 1 && BN * CPR == IPW * kWave * GW, "tile must split evenly into DMAs");
+    static_assert(2 * 4 * DT * kWave * 16 + 2 * kWave * 8 <= RING_BYTES,
+                  "the B merge fits group 1's ring");
+    static_assert(TILE_BYTES < 65536, "slot offsets are DS immediates");
+};
+
+template <typename E, int D>
+__global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel(
+    const sca_flash_params p, int num_q_tiles) {
+    using G = PairGeom<D>;
+    using M = Mfma<E>;
+    using vec8 = typename E::vec8;
+    constexpr int BN = G::BN;
+    constexpr int BM = G::BM;
+    constexpr int ROW_BYTES = G::ROW_BYTES;
+
+    extern __shared__ __align__(16) uint8_t lds8[];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int lane = tid % kWave;
+    const int lr = lane & 31;
+    const int hh = lane >> 5;
+    const int g = wave / G::GW;        // group
+    const int w4 = wave % G::GW;       // wave within the group
+    const int rg = w4 % 2;             // row group: rows 32*rg .. of the row tile
+    const int kq = w4 / 2;             // keys 32*kq .. of every key tile
+
+    // The groups share the workgroup barrier: every interval between two barriers is one
+    // pipeline step (or setup / merge phase) of each group. The group with fewer intervals
+    // pads with empty ones before the final merge, so both groups reach the same count.
+    int syncs = 0;
+    auto gsync = [&]() {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        ++syncs;
+    };
+
+    const int64_t bh_count = p.batch * p.num_heads;
+    const int64_t tile_linear = static_cast<int64_t>(blockIdx.x) / bh_count;
+    const int64_t bh = static_cast<int64_t>(blockIdx.x) % bh_count;
+    const int64_t b = bh / p.num_heads;
+    const int64_t h = bh % p.num_heads;
+    const int64_t h_kv = h / (p.num_heads / p.num_kv_heads);
+    const int seq_q = static_cast<int>(p.seq_q);
+    const int seq_kv = static_cast<int>(p.seq_kv);
+    const int diag = static_cast<int>(p.diagonal);
+    const float scale2 = p.scale * kLog2e;
+
+    const uint8_t* k_bytes = reinterpret_cast<const uint8_t*>(
+        static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh);
+    const uint8_t* v_bytes = reinterpret_cast<const uint8_t*>(
+        static_cast<const uint16_t*>(p.v) + b * p.v_sb + h_kv * p.v_sh);
+    const int k_row_bytes = static_cast<int>(p.k_ss) * 2;
+    const int v_row_bytes = static_cast<int>(p.v_ss) * 2;
+    const int k_records = (seq_kv - 1) * k_row_bytes + ROW_BYTES;
+    const int v_records = (seq_kv - 1) * v_row_bytes + ROW_BYTES;
+    uint32_t dma_koff[G::IPW], dma_voff[G::IPW];
+#pragma unroll
+    for (int i = 0; i < G::IPW; ++i) {
+        const int P = (w4 * G::IPW + i) * kWave + lane;
+        const int row = P / G::CPR;
+        const int pos = P % G::CPR;
+        dma_koff[i] = row * k_row_bytes + (pos ^ SwzK<D>(row)) * 16;
+        dma_voff[i] = row * v_row_bytes + (pos ^ SwzV<D>(row)) * 16;
+    }
+    uint8_t* const ring = lds8 + g * G::RING_BYTES;
+    // K tile t -> K slot t & 1, V tile t -> V slot t & 1 of this group's ring.
+    auto issue_k = [&](int t) {
+        uint8_t* dst = ring + (t & 1) * G::TILE_BYTES + w4 * G::IPW * 1024;
+        const uint32_t off = static_cast<uint32_t>(t * BN * k_row_bytes);
+#pragma unroll
+        for (int i = 0; i < G::IPW; ++i) DmaToLds(k_bytes, k_records, dst + i * 1024, dma_koff[i], off);
+    };
+    auto issue_v = [&](int t) {
+        uint8_t* dst = ring + (2 + (t & 1)) * G::TILE_BYTES + w4 * G::IPW * 1024;
+        const uint32_t off = static_cast<uint32_t>(t * BN * v_row_bytes);
+#pragma unroll
+        for (int i = 0; i < G::IPW; ++i) DmaToLds(v_bytes, v_records, dst + i * 1024, dma_voff[i], off);
+    };
+    // Fragment offsets, with the group's ring base folded in so slot offsets stay immediates.
+    const int wkey_base = 32 * kq;
+    const int k_row = wkey_base + lr;
+    uint32_t k_frag[G::KS];
+#pragma unroll
+    for (int ks = 0; ks < G::KS; ++ks) {
+        k_frag[ks] = g * G::RING_BYTES + k_row * ROW_BYTES + (((2 * ks) ^ hh ^ SwzK<D>(k_row)) * 16);
+    }
+    const int grp = lane >> 4;
+    const int sl = lane & 15;
+    const int v_key = wkey_base + 4 * hh + (sl >> 2);
+    const int v_chunk = 2 * (grp & 1) + ((sl & 3) >> 1);
+    const int v_half = (sl & 1) * 8;
+    uint32_t v_frag[G::DT];
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt) {
+        v_frag[dt] = g * G::RING_BYTES + v_key * ROW_BYTES +
+                     (((4 * dt + v_chunk) ^ SwzV<D>(v_key)) * 16) + v_half;
+    }
+
+    // Row tiles: A = T-1-t (long), B = t (short; none when they coincide).
+    const int qa = num_q_tiles - 1 - static_cast<int>(tile_linear);
+    const int qb = static_cast<int>(tile_linear);
+    const bool has_b = qb < qa;
+    auto key_tiles = [&](int qt, int& n, int& n_plain) {
+        const int q0 = qt * BM;
+        n = (seq_kv + BN - 1) / BN;
+        n_plain = seq_kv / BN;
+        const int last_key = q0 + BM - 1 + diag;
+        const int causal_tiles = last_key < 0 ? 0 : last_key / BN + 1;
+        if (causal_tiles < n) n = causal_tiles;
+        const int plain = (q0 + diag + 1) / BN;
+        if (plain < n_plain) n_plain = plain;
+        if (n_plain > n) n_plain = n;
+    };
+    int n_a, plain_a, n_b = 0, plain_b = 0;
+    key_tiles(qa, n_a, plain_a);
+    if (has_b) key_tiles(qb, n_b, plain_b);
+    // Group 0: A tiles [0, x). Group 1: B, its merge, then A tiles [x, n_a). A key range
+    // [kb, ke) takes ke - kb + 2 barrier intervals (two for its prologue), B's merge two, so
+    // x + 2 = (n_b + 2) + 2 + (n_a - x + 2) balances the groups.
+    int x = (n_a + n_b + (has_b ? 4 : 0) + 1) / 2;
+    if (x > n_a) x = n_a;
+    if (x < 1) x = 1;
+    const int syncs_g0 = x + 2;
+    const int syncs_g1 = (has_b ? n_b + 4 : 0) + (x < n_a ? n_a - x + 2 : 0);
+    const int syncs_all = syncs_g0 > syncs_g1 ? syncs_g0 : syncs_g1;
+
+    vec8 qf[G::KS];
+    auto load_q = [&](int qt) {
+        const int row = qt * BM + rg * 32 + lr;
+        const uint16_t* q_row = static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh +
+                                static_cast<int64_t>(row) * p.q_ss + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+            uint4 raw = make_uint4(0, 0, 0, 0);
+            if (row < seq_q) raw = *reinterpret_cast<const uint4*>(q_row + 16 * ks);
+            qf[ks] = __builtin_bit_cast(vec8, raw);
+        }
+    };
+
+    floatx16 o[G::DT];
+    float m_used, l_run;
+    auto reset_state = [&]() {
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
+        }
+        m_used = neg_inf();
+        l_run = 0.0f;
+    };
+
+    auto qk_slot = [&](int slot) {
+        const uint8_t* base = lds8 + slot * G::TILE_BYTES;
+        vec8 a[G::KS];
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) a[ks] = *reinterpret_cast<const vec8*>(base + k_frag[ks]);
+        floatx16 acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) acc = M::mma(a[ks], qf[ks], acc);
+        return acc;
+    };
+    auto pv_slot = [&](int slot, const uint32_t (&pw)[8]) {
+        const uint8_t* vbase = lds8 + slot * G::TILE_BYTES;
+        const vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+        const vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
+        vec8 va[G::DT][2];
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+            for (int ps = 0; ps < 2; ++ps) {
+                const uint2 lo = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps) * ROW_BYTES);
+                const uint2 hi = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps + 8) * ROW_BYTES);
+                va[dt][ps] = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+            o[dt] = M::mma(va[dt][0], pb0, o[dt]);
+            o[dt] = M::mma(va[dt][1], pb1, o[dt]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < G::DT; dt += 2) {
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+        }
+    };
+
+    // Key tiles [kb, ke) of row tile qt into the running state (o, m_used, l_run).
+    auto run_keys = [&](int qt, int kb, int ke, int n_plain) {
+        if (kb >= ke) return;
+        const int my_q = qt * BM + rg * 32 + lr;
+        // Prologue: K(kb), K(kb+1), V(kb); QK(kb) once K(kb) has landed.
+        issue_k(kb);
+        if (kb + 1 < ke) issue_k(kb + 1);
+        issue_v(kb);
+        if (kb + 1 < ke) {
+            WaitVm<2 * G::IPW>();
+        } else {
+            WaitVm<G::IPW>();
+        }
+        gsync();
+        floatx16 s_cur = qk_slot(kb & 1);
+        WaitVm<0>();
+        gsync();  // K(kb) read by every wave before step kb refills its slot
+        // Step j (S = j & 1): V(j+1) into V slot S^1 and K(j+2) into K slot S (both read in
+        // step j-1), QK(j+1) from K slot S^1 under the softmax of tile j, PV(j) from V slot S;
+        // then everything issued has landed before the group barrier.
+        auto step = [&]<int S>(int j, floatx16& s_in, floatx16& s_out) {
+            if (j + 1 < ke) issue_v(j + 1);
+            if (j + 2 < ke) issue_k(j + 2);
+            if (j + 1 < ke) s_out = qk_slot(S ^ 1);
+            floatx16 sv = s_in;
+            if (j >= n_plain) {
+                const int lim = min(seq_kv - 1, my_q + diag);
+                const int kbase = j * BN + wkey_base + 4 * hh;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = kbase + 8 * (i / 4) + (i % 4);
+                    sv[i] = key > lim ? neg_inf() : sv[i];
+                }
+            }
+            float tmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                               fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+            tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(sv[8], sv[9]), fmaxf(sv[10], sv[11])),
+                                     fmaxf(fmaxf(sv[12], sv[13]), fmaxf(sv[14], sv[15]))));
+            tmax = HalfMax(tmax) * scale2;
+            const bool grow = tmax > m_used + kRescaleSlack;
+            const float m_new = grow ? tmax : m_used;
+            const float alpha = grow ? fast_exp2(m_used - m_new) : 1.0f;
+            m_used = m_new;
+            l_run *= alpha;
+            const float mu = (m_used == neg_inf()) ? 0.0f : m_used;
+            uint32_t pw[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float p0 = fast_exp2(fmaf(sv[2 * i], scale2, -mu));
+                const float p1 = fast_exp2(fmaf(sv[2 * i + 1], scale2, -mu));
+                pw[i] = M::pack(p0, p1);
+                l_run = M::sum2(pw[i], l_run);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(pw[i]));
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, G::KS / 2, 0);
+#pragma unroll
+            for (int i = 0; i < G::KS; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSchedValu, 10, 0);
+                if (i == 0) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, G::KS - G::KS / 2, 0);
+            }
+            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+                for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+                }
+            }
+            pv_slot(2 + S, pw);
+            WaitVm<0>();
+            gsync();
+        };
+        floatx16 s_next;
+        int j = kb;
+        if (j & 1) {
+            step.template operator()<1>(j, s_cur, s_next);
+            s_cur = s_next;
+            ++j;
+        }
+        for (; j + 2 <= ke; j += 2) {
+            step.template operator()<0>(j, s_cur, s_next);
+            step.template operator()<1>(j + 1, s_next, s_cur);
+        }
+        if (j < ke) step.template operator()<0>(j, s_cur, s_next);
+    };
+
+    float4* const mquad = reinterpret_cast<float4*>(lds8);
+    if (g == 0) {
+        load_q(qa);
+        reset_state();
+        run_keys(qa, 0, x, plain_a);
+    } else {
+        if (has_b) {
+            load_q(qb);
+            reset_state();
+            run_keys(qb, 0, n_b, plain_b);
+            // B's two key halves meet here: the kq = 1 waves hand their state to kq = 0
+            // through group 1's ring (idle now: the last step's barrier retired every read).
+            float4* const bq = reinterpret_cast<float4*>(ring);
+            float2* const bst = reinterpret_cast<float2*>(bq + 2 * 4 * G::DT * kWave);
+            if (kq == 1) {
+#pragma unroll
+                for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        bq[(rg * 4 * G::DT + 4 * dt + q4) * kWave + lane] =
+                            make_float4(o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2],
+                                        o[dt][4 * q4 + 3]);
+                    }
+                }
+                bst[rg * kWave + lane] = make_float2(m_used, l_run);
+            }
+            gsync();
+            if (kq == 0) {
+                const float2 st = bst[rg * kWave + lane];
+                const float mm = fmaxf(m_used, st.x);
+                const float w0 = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
+                const float w1 = (st.x == neg_inf()) ? 0.0f : fast_exp2(st.x - mm);
+                const float l_tot = HalfSum(l_run * w0 + st.y * w1);
+                const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+                const int row = qb * BM + rg * 32 + lr;
+                const bool row_ok = row < seq_q;
+                uint16_t* out_row = static_cast<uint16_t*>(p.out) + b * p.o_sb + h * p.o_sh +
+                                    static_cast<int64_t>(row) * p.o_ss;
+#pragma unroll
+                for (int dt = 0; dt < G::DT; ++dt) {
+                    float acc[16];
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        const float4 v = bq[(rg * 4 * G::DT + 4 * dt + q4) * kWave + lane];
+                        acc[4 * q4] = o[dt][4 * q4] * w0 + v.x * w1;
+                        acc[4 * q4 + 1] = o[dt][4 * q4 + 1] * w0 + v.y * w1;
+                        acc[4 * q4 + 2] = o[dt][4 * q4 + 2] * w0 + v.z * w1;
+                        acc[4 * q4 + 3] = o[dt][4 * q4 + 3] * w0 + v.w * w1;
+                    }
+                    if (row_ok) {
+#pragma unroll
+                        for (int q4 = 0; q4 < 4; ++q4) {
+                            const int d0 = 32 * dt + 8 * q4 + 4 * hh;
+                            const uint32_t lo = M::pack(acc[4 * q4] * inv, acc[4 * q4 + 1] * inv);
+                            const uint32_t hi = M::pack(acc[4 * q4 + 2] * inv, acc[4 * q4 + 3] * inv);
+                            *reinterpret_cast<uint2*>(out_row + d0) = make_uint2(lo, hi);
+                        }
+                    }
+                }
+                if (row_ok && p.lse != nullptr && hh == 0) {
+                    p.lse[(b * p.num_heads + h) * p.seq_q + row] =
+                        l_tot > 0.0f ? (mm + __log2f(l_tot)) * kLn2 : neg_inf();
+                }
+            }
+            gsync();  // the merge buffer is the ring of the next key range
+        }
+        load_q(qa);
+        reset_state();
+        run_keys(qa, x, n_a, plain_a);
+    }
+
+    // Both groups reach the same barrier count (the counts are uniform per group).
+    while (syncs < syncs_all) gsync();
+
+    // A's four states per row group (groups 0 and 1, key halves 0 and 1) merge into the
+    // (g = 0, kq = 0) wave of the row group; the other three hand theirs over through LDS.
+    __syncthreads();
+    float2* const mstat = reinterpret_cast<float2*>(mquad + G::MERGE_QUADS);
+    const int src = g * 2 + kq;  // 0 = the merging wave
+    if (src != 0) {
+        float4* mbuf = mquad + ((rg * 3 + src - 1) * 4 * G::DT) * kWave + lane;
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                mbuf[(4 * dt + q4) * kWave] = make_float4(o[dt][4 * q4], o[dt][4 * q4 + 1],
+                                                          o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]);
+            }
+        }
+        mstat[(rg * 3 + src - 1) * kWave + lane] = make_float2(m_used, l_run);
+    }
+    __syncthreads();
+    if (src == 0) {
+        float2 st[3];
+#pragma unroll
+        for (int q = 0; q < 3; ++q) st[q] = mstat[(rg * 3 + q) * kWave + lane];
+        float mm = m_used;
+#pragma unroll
+        for (int q = 0; q < 3; ++q) mm = fmaxf(mm, st[q].x);
+        float wq[4];
+        wq[0] = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
+        float l = l_run * wq[0];
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+            wq[q + 1] = (st[q].x == neg_inf()) ? 0.0f : fast_exp2(st[q].x - mm);
+            l += st[q].y * wq[q + 1];
+        }
+        const float l_tot = HalfSum(l);
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        const int row = qa * BM + rg * 32 + lr;
+        const bool row_ok = row < seq_q;
+        uint16_t* out_row = static_cast<uint16_t*>(p.out) + b * p.o_sb + h * p.o_sh +
+                            static_cast<int64_t>(row) * p.o_ss;
+        const float4* mb = mquad + (rg * 3 * 4 * G::DT) * kWave + lane;
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+            float acc[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] = o[dt][i] * wq[0];
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const float4 v = mb[(q * 4 * G::DT + 4 * dt + q4) * kWave];
+                    acc[4 * q4] += v.x * wq[q + 1];
+                    acc[4 * q4 + 1] += v.y * wq[q + 1];
+                    acc[4 * q4 + 2] += v.z * wq[q + 1];
+                    acc[4 * q4 + 3] += v.w * wq[q + 1];
+                }
+            }
+            if (row_ok) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int d0 = 32 * dt + 8 * q4 + 4 * hh;
+                    const uint32_t lo = M::pack(acc[4 * q4] * inv, acc[4 * q4 + 1] * inv);
+                    const uint32_t hi = M::pack(acc[4 * q4 + 2] * inv, acc[4 * q4 + 3] * inv);
+                    *reinterpret_cast<uint2*>(out_row + d0) = make_uint2(lo, hi);
+                }
+            }
+        }
+        if (row_ok && p.lse != nullptr && hh == 0) {
+            p.lse[(b * p.num_heads + h) * p.seq_q + row] =
+                l_tot > 0.0f ? (mm + __log2f(l_tot)) * kLn2 : neg_inf();
+        }
+    }
+}
+
 template <typename E, int D, bool kCausal>
 int LaunchFlash(const sca_flash_params& p, hipStream_t s);
 
@@ -1123,6 +1578,42 @@ int LaunchFlash(const sca_flash_params& p, hipStream_t s) {
     return CheckLaunch("flash_fwd_kernel", s);
 }
 
+template <typename E, int D>
+int LaunchFlashPair(const sca_flash_params& p, hipStream_t s) {
+    using G = PairGeom<D>;
+    const int64_t extent_k = (p.seq_kv + 4 * G::BN) * p.k_ss * 2;
+    const int64_t extent_v = (p.seq_kv + 4 * G::BN) * p.v_ss * 2;
+    if (extent_k >= (1LL << 31) || extent_v >= (1LL << 31)) return LaunchFlash<E, D, true>(p, s);
+    const int64_t num_q_tiles = (p.seq_q + G::BM - 1) / G::BM;
+    const int64_t blocks = (num_q_tiles + 1) / 2 * p.batch * p.num_heads;
+    if (blocks <= 0) return 0;
+    if (blocks > 0x7fffffffLL) {
+        return SetError(SCA_E_SEQ_TOO_LONG, "flash: grid of " + std::to_string(blocks) +
+                                                " workgroups exceeds the launch limit");
+    }
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t err = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&flash_fwd_pair_kernel<E, D>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
+        if (err != hipSuccess) (void)hipGetLastError();
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((flash_fwd_pair_kernel<E, D>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(G::THREADS), G::LDS_BYTES, s, p, static_cast<int>(num_q_tiles));
+    return CheckLaunch("flash_fwd_pair_kernel", s);
+}
+
+// Small causal grids (64-row tiles in complementary pairs) run the two-group pair kernel;
+// SCA_FLASH_PAIR=0 selects the 8-wave paired pass kernel instead, for measurement.
+bool UsePairKernel() {
+    static const bool on = [] {
+        const char* env = std::getenv("SCA_FLASH_PAIR");
+        return env == nullptr || std::atoi(env) != 0;
+    }();
+    return on;
+}
+
 // Row groups of the DMA kernel. Non-causal: 4 (128-row workgroups, the least K/V traffic per
 // FLOP). Causal: 2 (64-row workgroups that each take a complementary pair of row tiles, so every
 // workgroup gets the same share of the triangle) while the 128-row grid would give fewer than two
@@ -1152,10 +1643,16 @@ int LaunchForDim(const sca_flash_params& p, hipStream_t s) {
     switch (p.head_dim) {
         case 32: return LaunchFlash<E, 32, kCausal>(p, s);
         case 64:
+            if (kCausal && UsePairKernel() && DmaRowGroups(p, kCausal) == 2) {
+                return LaunchFlashPair<E, 64>(p, s);
+            }
             return DmaRowGroups(p, kCausal) == 2 ? LaunchFlashDma<E, 64, 2, kCausal>(p, s)
                                                  : LaunchFlashDma<E, 64, 4, kCausal>(p, s);
         case 96: return LaunchFlash<E, 96, kCausal>(p, s);
         case 128:
+            if (kCausal && UsePairKernel() && DmaRowGroups(p, kCausal) == 2) {
+                return LaunchFlashPair<E, 128>(p, s);
+            }
             return DmaRowGroups(p, kCausal) == 2 ? LaunchFlashDma<E, 128, 2, kCausal>(p, s)
                                                  : LaunchFlashDma<E, 128, 4, kCausal>(p, s);
         case 160: return LaunchFlash<E, 160, kCausal>(p, s);

@@ -69,6 +69,15 @@ def test_lse_matches_logsumexp(hip):
     _case("bf16", True, 2, 8, 2, 100, 300, 128, 50124, want_lse=True)
 
 
+@pytest.mark.parametrize("sq,skv,D,dtype", [(320, 320, 128, "f16"), (448, 512, 64, "bf16"),
+                                            (577, 700, 128, "bf16"), (64, 64, 128, "f16")])
+def test_causal_two_group_pairs(hip, sq, skv, D, dtype):
+    # Small causal grids run complementary 64-row tiles in two wave groups: odd tile counts
+    # leave a middle tile split between the groups, skv > sq moves the diagonal, and the long
+    # tile's two halves and the short tile are written by different waves (output and LSE).
+    _case(dtype, True, 1, 4, 2, sq, skv, D, 51000 + sq + D, want_lse=True)
+
+
 def test_bshd_layout_equals_bhsd(hip):
     B, Hq, Hkv, S, D = 2, 8, 4, 200, 128
     q, k, v = uniform((B, Hq, S, D), 7), uniform((B, Hkv, S, D), 8), uniform((B, Hkv, S, D), 9)
