@@ -1090,7 +1090,6 @@ struct PairGeom {
     static constexpr int TILE_BYTES = BN * D * 2;
     static constexpr int IPW = BN * CPR / (kWave * GW);  // DMA instructions per wave per tile
     static constexpr int RING_BYTES = 4 * TILE_BYTES;    // K slots 0, 1, then V slots 0, 1
-    static constexpr int MERGE_FLOATS = DT * 16 + 2;
     // Final merge: per row group, three partial states (16-byte quads) and their (m, l).
     static constexpr int MERGE_QUADS = 2 * 3 * 4 * DT * kWave;
     static constexpr int MERGE_BYTES = MERGE_QUADS * 16 + 2 * 3 * kWave * 8;
