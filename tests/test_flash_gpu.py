@@ -78,6 +78,16 @@ def test_causal_two_group_pairs(hip, sq, skv, D, dtype):
     _case(dtype, True, 1, 4, 2, sq, skv, D, 51000 + sq + D, want_lse=True)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,sq,skv,D,dtype", [
+    (2, 8, 2, 193, 450, 64, "bf16"),    # GQA group 4, two batches, ragged rows and keys
+    (1, 8, 8, 1, 700, 128, "f16"),      # one query row far below the diagonal
+    (1, 2, 1, 1473, 1473, 128, "f16"),  # 24 row tiles with a 1-row tail, 12 pairs
+    (3, 4, 4, 130, 130, 64, "f16"),     # three tiles: one pair and a lone middle tile
+])
+def test_causal_two_group_pairs_shapes(hip, B, Hq, Hkv, sq, skv, D, dtype):
+    _case(dtype, True, B, Hq, Hkv, sq, skv, D, 52000 + sq + skv + D, want_lse=True)
+
+
 def test_bshd_layout_equals_bhsd(hip):
     B, Hq, Hkv, S, D = 2, 8, 4, 200, 128
     q, k, v = uniform((B, Hq, S, D), 7), uniform((B, Hkv, S, D), 8), uniform((B, Hkv, S, D), 9)
