@@ -68,6 +68,18 @@ def dispatcher_splits(batch, Hq, Hkv, seq_kv, D):
     return SH.decode_splits(SH.AttentionShape(batch, 1, seq_kv, Hq, Hkv, D), cus)
 
 
+def prewarm(launch, seconds):
+    """Untimed launches for `seconds`: the device's clocks ramp up under sustained load, so each
+    timed leg starts from the operating point a busy device runs at."""
+    if seconds <= 0:
+        return
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            launch()
+        sca_amd.synchronize()
+
+
 def time_launches(launch, steps, warmup):
     for _ in range(warmup):
         launch()
@@ -96,7 +108,7 @@ def launch_percentiles(launch, runs=50):
 
 
 # ---- C2: flash prefill -------------------------------------------------------------------------
-def bench_flash(steps, warmup, causal, B=1, Hh=8, S=4096, D=128):
+def bench_flash(steps, warmup, causal, B=1, Hh=8, S=4096, D=128, prewarm_s=0.0):
     rng = np.random.default_rng(2024)
     dq = H.DeviceBuffer.from_array(f16_bits(rng, (B, Hh, S, D)))
     dk = H.DeviceBuffer.from_array(f16_bits(rng, (B, Hh, S, D)))
@@ -113,6 +125,7 @@ def bench_flash(steps, warmup, causal, B=1, Hh=8, S=4096, D=128):
     p.causal = 1 if causal else 0
     p.dtype = H.DTYPE_F16
     p.diagonal = 0
+    prewarm(lambda: H.flash_fwd(p), prewarm_s)
     ms = time_launches(lambda: H.flash_fwd(p), steps, warmup)
     flops = causal_flops(B, Hh, S, D) if causal else 4 * B * Hh * S * S * D
     pct = launch_percentiles(lambda: H.flash_fwd(p))
@@ -121,7 +134,7 @@ def bench_flash(steps, warmup, causal, B=1, Hh=8, S=4096, D=128):
 
 
 # ---- C3: GQA causal prefill (reported next to the headline) -----------------------------------
-def bench_flash_gqa(steps, warmup, B=4, Hq=32, Hkv=8, S=8192, D=128):
+def bench_flash_gqa(steps, warmup, B=4, Hq=32, Hkv=8, S=8192, D=128, prewarm_s=0.0):
     """C3: bf16 Q/K/V ~ N(0, 0.5^2), causal, group 4; flash through the C ABI."""
     rng = np.random.default_rng(2025)
     dq = H.DeviceBuffer.from_array(bf16_bits(rng, (B, Hq, S, D), std=0.5))
@@ -139,13 +152,14 @@ def bench_flash_gqa(steps, warmup, B=4, Hq=32, Hkv=8, S=8192, D=128):
     p.causal = 1
     p.dtype = H.DTYPE_BF16
     p.diagonal = 0
+    prewarm(lambda: H.flash_fwd(p), prewarm_s)
     ms = time_launches(lambda: H.flash_fwd(p), steps, warmup)
     flops = causal_flops(B, Hq, S, D)
     return {"ms": ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
 # ---- C4: split-K decode --------------------------------------------------------------------------
-def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=None):
+def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=None, prewarm_s=0.0):
     if splits is None:
         splits = dispatcher_splits(B, Hq, Hkv, S, D)
     rng = np.random.default_rng(4004)
@@ -165,13 +179,15 @@ def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=None):
     p.o_sb, p.o_sh = Hq * D, D
     p.scale = float(np.float32(1.0 / np.sqrt(D)))
     p.dtype = H.DTYPE_F16
+    prewarm(lambda: H.decode_splitk(p), prewarm_s)
     ms = time_launches(lambda: H.decode_splitk(p), steps, warmup)
     nbytes = 2 * B * Hkv * S * D * 2 + 2 * B * Hq * D * 2
     return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9, "splits": splits}
 
 
 # ---- C5: paged decode ------------------------------------------------------------------------------
-def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=512, hi=16384):
+def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=512, hi=16384,
+                prewarm_s=0.0):
     rng = np.random.default_rng(5005)
     lengths = rng.integers(lo, hi + 1, size=num_seqs).astype(np.int64)
     final = lengths + steps
@@ -193,12 +209,10 @@ def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=
     dt = H.DeviceBuffer.from_array(table)
     dq = H.DeviceBuffer.from_array(bf16_bits(rng, (num_seqs, Hq, 1, D)))
     dout = H.DeviceBuffer(num_seqs * Hq * D * 2)
-    dlens = H.DeviceBuffer(num_seqs * 4)
     parts = H.DeviceBuffer(4 * sca_amd.hip_lib().sca_hip_decode_partial_elements(num_seqs, Hq,
                                                                                   splits, D))
     new_k = H.DeviceBuffer.from_array(bf16_bits(rng, (num_seqs, Hkv, D)))
     new_v = H.DeviceBuffer.from_array(bf16_bits(rng, (num_seqs, Hkv, D)))
-    dslots = H.DeviceBuffer(num_seqs * 4)
     shape = H.KvShape()
     shape.num_blocks, shape.block_size, shape.num_kv_heads, shape.head_dim = num_blocks, bs, Hkv, D
     p = H.DecodeParams()
@@ -214,31 +228,41 @@ def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=
     p.scale = float(np.float32(1.0 / np.sqrt(D)))
     p.dtype = H.DTYPE_BF16
     p.page_table, p.block_size, p.max_blocks_per_seq = dt.ptr, bs, max_blocks
-    p.num_kv_blocks, p.seq_lens = num_blocks, dlens.ptr
+    p.num_kv_blocks = num_blocks
     dorder = H.DeviceBuffer(num_seqs * 8)
     p.batch_order = dorder.ptr
     L = sca_amd.hip_lib()
-    cur = lengths.copy()
-    total_ms, total_bytes = 0.0, 0
-    start, stop = H.Event(), H.Event()
-    for step in range(steps + 2):  # two untimed warmup steps on the starting lengths
+    # Every step's slots and lengths are computed up front and uploaded once, so the steps are
+    # enqueued back to back, as in a decode loop over many layers: step t appends one token per
+    # sequence at position lengths + t, then attends over lengths + t + 1 tokens. Two untimed
+    # warmup steps attend over the starting lengths first.
+    all_lens = np.stack([lengths] * 2 + [lengths + t + 1 for t in range(steps)]).astype(np.int32)
+    all_slots = np.stack([table[np.arange(num_seqs), (lengths + t) // bs].astype(np.int64) * bs
+                          + (lengths + t) % bs for t in range(steps)]).astype(np.int32)
+    dlens_all = H.DeviceBuffer.from_array(all_lens)
+    dslots_all = H.DeviceBuffer.from_array(all_slots)
+    p.seq_lens = dlens_all.ptr  # the starting lengths
+    prewarm(lambda: H.decode_splitk_paged(p), prewarm_s)
+    events = [(H.Event(), H.Event()) for _ in range(steps)]
+    total_bytes = 0
+    for step in range(steps + 2):
         timed = step >= 2
         if timed:
-            # append one token per sequence at position cur[s] (slot from the block table)
-            slots = (table[np.arange(num_seqs), cur // bs].astype(np.int64) * bs + cur % bs)
-            dslots.upload(slots.astype(np.int32))
-            H.check(L.sca_hip_kv_append(dk.ptr, dv.ptr, new_k.ptr, new_v.ptr, dslots.ptr,
-                                        num_seqs, shape, 2, None))
-            cur = cur + 1
-        dlens.upload(cur.astype(np.int32))
-        start.record()
-        H.decode_splitk_paged(p)
-        stop.record()
-        stop.synchronize()
-        if timed:
-            total_ms += start.elapsed_ms(stop)
+            t = step - 2
+            H.check(L.sca_hip_kv_append(dk.ptr, dv.ptr, new_k.ptr, new_v.ptr,
+                                        dslots_all.ptr + 4 * t * num_seqs, num_seqs, shape, 2,
+                                        None))
+            cur = all_lens[step].astype(np.int64)
             total_bytes += int(cur.sum()) * Hkv * D * 2 * 2 + int(((cur + bs - 1) // bs).sum()) * 4 \
                 + 2 * num_seqs * Hq * D * 2
+        p.seq_lens = dlens_all.ptr + 4 * step * num_seqs
+        if timed:
+            events[step - 2][0].record()
+        H.decode_splitk_paged(p)
+        if timed:
+            events[step - 2][1].record()
+    events[-1][1].synchronize()
+    total_ms = sum(a.elapsed_ms(b) for a, b in events)
     ms = total_ms / steps
     nbytes = total_bytes / steps
     return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9, "splits": splits,
@@ -393,6 +417,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--paged-steps", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prewarm", type=float, default=0.5,
+                    help="seconds of untimed launches of each leg's own work before it is timed")
     ap.add_argument("--only", default="all",
                     help="comma list of prefill, gqa, paged, paged_host, decode, copy "
                          "(default: all but copy)")
@@ -413,16 +439,16 @@ def main():
 
     res = {}
     if "prefill" in parts:
-        res["c2_causal"] = bench_flash(args.steps, args.warmup, True)
+        res["c2_causal"] = bench_flash(args.steps, args.warmup, True, prewarm_s=args.prewarm)
         res["c2_noncausal"] = bench_flash(args.steps, args.warmup, False)
     if "gqa" in parts:
-        res["c3_gqa"] = bench_flash_gqa(max(5, args.steps // 5), 3)
+        res["c3_gqa"] = bench_flash_gqa(max(5, args.steps // 5), 3, prewarm_s=args.prewarm)
     if "paged" in parts:
-        res["c5_paged"] = bench_paged(args.paged_steps)
+        res["c5_paged"] = bench_paged(args.paged_steps, prewarm_s=args.prewarm)
     if "paged_host" in parts:
         res["c5_host"] = bench_paged_host(args.paged_steps)
     if "decode" in parts:
-        res["c4_decode"] = bench_decode(args.steps, args.warmup)
+        res["c4_decode"] = bench_decode(args.steps, args.warmup, prewarm_s=args.prewarm)
     if "copy" in parts:
         res["copy"] = bench_copy(args.steps, args.warmup)
 
