@@ -1614,10 +1614,10 @@ bool UsePairKernel() {
 }
 
 // Row groups of the DMA kernel. Non-causal: 4 (128-row workgroups, the least K/V traffic per
-// FLOP). Causal: 2 (64-row workgroups that each take a complementary pair of row tiles, so every
-// workgroup gets the same share of the triangle) while the 128-row grid would give fewer than two
-// workgroups per CU to balance over, else 4. SCA_FLASH_ROW_GROUPS (2 or 4) overrides the choice,
-// for measurement.
+// FLOP). Causal: 2 (64-row tiles taken in complementary pairs, so every workgroup gets the same
+// share of the triangle) while the pairs fit one workgroup per CU (the pair kernel) or fewer
+// than two per CU (the 8-wave kernel, SCA_FLASH_PAIR=0); beyond that the longest-first 128-row
+// grid balances better. SCA_FLASH_ROW_GROUPS (2 or 4) overrides the choice, for measurement.
 int DmaRowGroups(const sca_flash_params& p, bool causal) {
     if (const char* env = std::getenv("SCA_FLASH_ROW_GROUPS")) {
         const int v = std::atoi(env);
@@ -1634,7 +1634,10 @@ int DmaRowGroups(const sca_flash_params& p, bool causal) {
         return n > 0 ? n : 256;
     }();
     const int64_t tiles128 = (p.seq_q + 127) / 128 * p.batch * p.num_heads;
-    return tiles128 < 2 * static_cast<int64_t>(cu_count) ? 2 : 4;
+    // One pair per 128-row tile: tiles128 pairs of 64-row tiles.
+    const int64_t pair_limit = UsePairKernel() ? static_cast<int64_t>(cu_count)
+                                               : 2 * static_cast<int64_t>(cu_count) - 1;
+    return tiles128 <= pair_limit ? 2 : 4;
 }
 
 template <typename E, bool kCausal>
