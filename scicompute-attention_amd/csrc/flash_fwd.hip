@@ -1301,13 +1301,15 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
         floatx16 s_cur = qk_slot(kb & 1);
         WaitVm<0>();
         gsync();  // K(kb) read by every wave before step kb refills its slot
-        // Step j (S = j & 1): V(j+1) into V slot S^1 and K(j+2) into K slot S (both read in
+        // Step j (S = j & 1): K(j+2) into K slot S and V(j+1) into V slot S^1 (both read in
         // step j-1), QK(j+1) from K slot S^1 under the softmax of tile j, PV(j) from V slot S;
-        // then everything issued has landed before the group barrier.
+        // then everything issued has landed before the group barrier. V's DMAs are issued
+        // behind the K fragment reads of QK(j+1), so those start sooner (2-3% faster than
+        // issuing both tiles first).
         auto step = [&]<int S>(int j, floatx16& s_in, floatx16& s_out) {
-            if (j + 1 < ke) issue_v(j + 1);
             if (j + 2 < ke) issue_k(j + 2);
             if (j + 1 < ke) s_out = qk_slot(S ^ 1);
+            if (j + 1 < ke) issue_v(j + 1);
             floatx16 sv = s_in;
             if (j >= n_plain) {
                 const int lim = min(seq_kv - 1, my_q + diag);
