@@ -171,3 +171,54 @@ def test_large_ragged_batch_ranked_through_scratch(hip):
     lengths = rng.integers(0, 90, size=300).tolist()
     _case(lengths, 16, 8, 2, 64, "f16", 86001, splits=2)
     _case(lengths, 16, 8, 2, 64, "f16", 86002, splits=3, longest_first=False)
+
+
+
+def _bf16_normal(rng, shape):
+    """bf16 bit patterns of N(0, 1) samples (upper half of the fp32 word)."""
+    f = rng.standard_normal(int(np.prod(shape)), dtype=np.float32)
+    return (f.view(np.uint32) >> 16).astype(np.uint16).reshape(shape)
+
+
+def _bf16_to_f32(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def test_c5_full_size_against_fp32(hip):
+    """C5 at its full shape (64 sequences, L ~ U[512, 16384], bs 16, Hq 32, Hkv 8, D 128, bf16,
+    12 splits as the dispatcher picks them, permuted block table, 2.2 GB pool). Each sequence
+    is checked against an fp32 softmax(q k^T * scale) v over the rows its block table gathers
+    (page_table.cuh:18-36), within the bf16 tolerance of the other paged cases (max abs error
+    <= 1.6e-2 of max |ref|)."""
+    S, bs, Hq, Hkv, D, splits = 64, 16, 32, 8, 128, 12
+    rng = np.random.default_rng(5005)
+    lengths = rng.integers(512, 16384 + 1, size=S).astype(np.int64)
+    need = (lengths + bs - 1) // bs
+    nb = int(need.sum()) + 64
+    perm = rng.permutation(nb).astype(np.int32)
+    table = np.full((S, int(need.max())), -1, np.int32)
+    pos = 0
+    for s in range(S):
+        table[s, :need[s]] = perm[pos:pos + need[s]]
+        pos += need[s]
+    kb = _bf16_normal(rng, (nb * bs, Hkv, D))
+    vb = _bf16_normal(rng, (nb * bs, Hkv, D))
+    qb = _bf16_normal(rng, (S, Hq, 1, D))
+    print(f"paged C5 full size: seqs={S} pool blocks={nb} splits={splits}", flush=True)
+    got = run_paged(qb, kb, vb, table, lengths.tolist(), "bf16", Hq=Hq, Hkv=Hkv, D=D, bs=bs,
+                    num_blocks=nb, splits=splits)
+
+    scale = np.float32(1.0 / np.sqrt(D))
+    qf = _bf16_to_f32(qb).reshape(S, Hkv, Hq // Hkv, D)  # query heads grouped by KV head
+    ref = np.empty((S, Hq, D), np.float64)
+    for s in range(S):
+        L = int(lengths[s])
+        idx = (table[s, :need[s]].astype(np.int64)[:, None] * bs + np.arange(bs)).reshape(-1)[:L]
+        ks = _bf16_to_f32(kb[idx]).transpose(1, 0, 2)  # [Hkv, L, D]
+        vs = _bf16_to_f32(vb[idx]).transpose(1, 0, 2)
+        sc = np.matmul(qf[s], ks.transpose(0, 2, 1)) * scale  # [Hkv, group, L]
+        sc -= sc.max(axis=-1, keepdims=True)
+        w = np.exp(sc)
+        w /= w.sum(axis=-1, keepdims=True)
+        ref[s] = np.matmul(w, vs).reshape(Hq, D)
+    check_attention(got.reshape(-1, D), ref.reshape(-1, D), "bf16", "paged C5 full size")
