@@ -248,13 +248,15 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_partial_kernel(const sc
     const int64_t v_row_bytes = p.v_ss * kElemBytes;
 
     // Segment loop (one segment for contiguous KV; page-table segments staged in LDS otherwise).
-    const int64_t seg_tokens = kPaged ? static_cast<int64_t>(kPageSegment) * p.block_size
-                                      : (t_end - t_begin);
-    for (int64_t seg = t_begin; seg < t_end; seg += (seg_tokens > 0 ? seg_tokens : 1)) {
-        const int64_t seg_end = (seg + seg_tokens < t_end) ? seg + seg_tokens : t_end;
+    // A paged segment ends on a page boundary, so it never spans more than kPageSegment pages
+    // whatever page offset the split starts at.
+    int64_t seg_end = t_begin;
+    for (int64_t seg = t_begin; seg < t_end; seg = seg_end) {
         int64_t page0 = 0;
         if constexpr (kPaged) {
             page0 = seg / p.block_size;
+            const int64_t cap = (page0 + kPageSegment) * p.block_size;
+            seg_end = cap < t_end ? cap : t_end;
             const int64_t page_last = (seg_end - 1) / p.block_size;
             const int64_t n_pages = page_last - page0 + 1;
             __syncthreads();
@@ -268,6 +270,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_partial_kernel(const sc
                 s_pages[i] = id;
             }
             __syncthreads();
+        } else {
+            seg_end = t_end;
         }
 
         for (int64_t base = seg; base < seg_end; base += RG * kChunk) {
@@ -631,13 +635,16 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_mfma_kernel(const sca_d
     const int tr_rd = wave_off + tr_row * G::RB + 8 * (col % 4);
     const int tr_x = VSwz<D>(tr_row) * 32;
 
-    const int64_t seg_tokens = kPaged ? (static_cast<int64_t>(kPageSegment) << block_shift)
-                                      : (t_end - t_begin);
-    for (int64_t seg = t_begin; seg < t_end; seg += (seg_tokens > 0 ? seg_tokens : 1)) {
-        const int64_t seg_end = (seg + seg_tokens < t_end) ? seg + seg_tokens : t_end;
+    // A paged segment ends on a page boundary, so it never spans more than kPageSegment pages
+    // whatever page offset the split starts at.
+    int64_t seg_end = t_begin;
+    for (int64_t seg = t_begin; seg < t_end; seg = seg_end) {
         int64_t page0 = 0;
+        seg_end = t_end;
         if constexpr (kPaged) {
             page0 = seg >> block_shift;
+            const int64_t cap = (page0 + kPageSegment) << block_shift;
+            seg_end = cap < t_end ? cap : t_end;
             const int64_t n_pages = ((seg_end - 1) >> block_shift) - page0 + 1;
             __syncthreads();
             for (int64_t i = threadIdx.x; i < n_pages; i += kDecodeThreads) {
@@ -900,22 +907,32 @@ __global__ __launch_bounds__(256) void decode_order_kernel(const int32_t* seq_le
     order[2 * rank + 1] = mine;
 }
 
-// SCA_DECODE_MFMA=0 selects the VALU kernels for every shape (measurement and comparison).
+// The MFMA kernel serves every shape it covers. A measurement build (-DSCA_MEASUREMENT_BUILD)
+// reads SCA_DECODE_MFMA=0 to select the VALU kernels instead; the shipped library ignores it.
 bool MfmaDecodeEnabled() {
+#ifdef SCA_MEASUREMENT_BUILD
     static const bool enabled = [] {
         const char* v = std::getenv("SCA_DECODE_MFMA");
         return v == nullptr || v[0] != '0';
     }();
     return enabled;
+#else
+    return true;
+#endif
 }
 
-// Head slot per wave (SCA_DECODE_WAVE_HEADS=1/0 forces it on/off; default: paged only).
+// Head slot per wave for paged KV, four waves per slot for contiguous KV. A measurement build
+// reads SCA_DECODE_WAVE_HEADS=1/0 to force either.
 bool MfmaWaveHeads(bool paged) {
+#ifdef SCA_MEASUREMENT_BUILD
     static const int mode = [] {
         const char* v = std::getenv("SCA_DECODE_WAVE_HEADS");
         return v == nullptr ? -1 : (v[0] == '0' ? 0 : 1);
     }();
     return mode < 0 ? paged : mode == 1;
+#else
+    return paged;
+#endif
 }
 
 template <typename E, int D, bool kPaged>

@@ -1540,13 +1540,9 @@ int LaunchFlashDma(const sca_flash_params& p, hipStream_t s) {
         return SetError(SCA_E_SEQ_TOO_LONG, "flash: grid of " + std::to_string(blocks) +
                                                 " workgroups exceeds the launch limit");
     }
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t err = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&flash_fwd_dma_kernel<E, D, RG, KQ, kCausal, false>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
-        if (err != hipSuccess) (void)hipGetLastError();
-        attr_set = true;
+    if (const int rc =
+            EnsureLdsLimit<&flash_fwd_dma_kernel<E, D, RG, KQ, kCausal, false>>(G::LDS_BYTES, "flash LDS limit")) {
+        return rc;
     }
     hipLaunchKernelGGL((flash_fwd_dma_kernel<E, D, RG, KQ, kCausal, false>),
                        dim3(static_cast<unsigned>(blocks)), dim3(G::THREADS), G::LDS_BYTES, s, p,
@@ -1564,15 +1560,9 @@ int LaunchFlash(const sca_flash_params& p, hipStream_t s) {
         return SetError(SCA_E_SEQ_TOO_LONG, "flash: grid of " + std::to_string(blocks) +
                                                 " workgroups exceeds the launch limit");
     }
-    static bool attr_set = false;  // benign race: the attribute call is idempotent
-    if (!attr_set) {
-        const hipError_t err = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&flash_fwd_kernel<E, D, kCausal>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
-        // A refusal here is not fatal: the launch itself reports an LDS request the device
-        // cannot serve.
-        if (err != hipSuccess) (void)hipGetLastError();
-        attr_set = true;
+    if (const int rc =
+            EnsureLdsLimit<&flash_fwd_kernel<E, D, kCausal>>(G::LDS_BYTES, "flash LDS limit")) {
+        return rc;
     }
     hipLaunchKernelGGL((flash_fwd_kernel<E, D, kCausal>), dim3(static_cast<unsigned>(blocks)),
                        dim3(G::THREADS), G::LDS_BYTES, s, p, static_cast<int>(num_q_tiles));
@@ -1592,39 +1582,43 @@ int LaunchFlashPair(const sca_flash_params& p, hipStream_t s) {
         return SetError(SCA_E_SEQ_TOO_LONG, "flash: grid of " + std::to_string(blocks) +
                                                 " workgroups exceeds the launch limit");
     }
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t err = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&flash_fwd_pair_kernel<E, D>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
-        if (err != hipSuccess) (void)hipGetLastError();
-        attr_set = true;
+    if (const int rc =
+            EnsureLdsLimit<&flash_fwd_pair_kernel<E, D>>(G::LDS_BYTES, "flash LDS limit")) {
+        return rc;
     }
     hipLaunchKernelGGL((flash_fwd_pair_kernel<E, D>), dim3(static_cast<unsigned>(blocks)),
                        dim3(G::THREADS), G::LDS_BYTES, s, p, static_cast<int>(num_q_tiles));
     return CheckLaunch("flash_fwd_pair_kernel", s);
 }
 
-// Small causal grids (64-row tiles in complementary pairs) run the two-group pair kernel;
-// SCA_FLASH_PAIR=0 selects the 8-wave paired pass kernel instead, for measurement.
+// Small causal grids (64-row tiles in complementary pairs) run the two-group pair kernel. A
+// measurement build (-DSCA_MEASUREMENT_BUILD) reads SCA_FLASH_PAIR=0 to select the 8-wave
+// paired pass kernel instead; the shipped library ignores the variable.
 bool UsePairKernel() {
+#ifdef SCA_MEASUREMENT_BUILD
     static const bool on = [] {
         const char* env = std::getenv("SCA_FLASH_PAIR");
         return env == nullptr || std::atoi(env) != 0;
     }();
     return on;
+#else
+    return true;
+#endif
 }
 
 // Row groups of the DMA kernel. Non-causal: 4 (128-row workgroups, the least K/V traffic per
 // FLOP). Causal: 2 (64-row tiles taken in complementary pairs, so every workgroup gets the same
 // share of the triangle) while the pairs fit one workgroup per CU (the pair kernel) or fewer
 // than two per CU (the 8-wave kernel, SCA_FLASH_PAIR=0); beyond that the longest-first 128-row
-// grid balances better. SCA_FLASH_ROW_GROUPS (2 or 4) overrides the choice, for measurement.
+// grid balances better. In a measurement build SCA_FLASH_ROW_GROUPS (2 or 4) overrides the
+// choice.
 int DmaRowGroups(const sca_flash_params& p, bool causal) {
+#ifdef SCA_MEASUREMENT_BUILD
     if (const char* env = std::getenv("SCA_FLASH_ROW_GROUPS")) {
         const int v = std::atoi(env);
         if (v == 2 || v == 4) return v;
     }
+#endif
     if (!causal) return 4;
     static int cu_count = [] {
         int dev = 0, n = 0;
@@ -1702,13 +1696,9 @@ int LaunchFlashVarlen(const sca_flash_varlen_params& v, hipStream_t s) {
     p.scale = v.scale;
     p.causal = v.causal;
     p.dtype = v.dtype;
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t err = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&flash_fwd_dma_kernel<E, D, 4, 2, kCausal, true>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
-        if (err != hipSuccess) (void)hipGetLastError();
-        attr_set = true;
+    if (const int rc =
+            EnsureLdsLimit<&flash_fwd_dma_kernel<E, D, 4, 2, kCausal, true>>(G::LDS_BYTES, "flash LDS limit")) {
+        return rc;
     }
     hipLaunchKernelGGL((flash_fwd_dma_kernel<E, D, 4, 2, kCausal, true>),
                        dim3(static_cast<unsigned>(blocks)), dim3(G::THREADS), G::LDS_BYTES, s, p,

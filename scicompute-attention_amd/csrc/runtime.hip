@@ -27,13 +27,6 @@ bool DebugSync() {
     return enabled;
 }
 
-int FromHip(hipError_t err, const char* what) {
-    if (err == hipSuccess) return 0;
-    return SetError(static_cast<int>(err),
-                    std::string(what) + ": " + hipGetErrorName(err) + " (" +
-                        hipGetErrorString(err) + ")");
-}
-
 // Zero-fill with 16 B stores plus a byte tail. Used instead of hipMemsetAsync so that callers
 // that capture the stream into a graph record a kernel node, not a memset node.
 __global__ void zero_fill_kernel(uint8_t* dst, size_t bytes) {
@@ -56,6 +49,13 @@ __global__ void zero_fill_kernel(uint8_t* dst, size_t bytes) {
 int SetError(int code, const std::string& message) {
     g_last_error = message;
     return code;
+}
+
+int FromHip(hipError_t err, const char* what) {
+    if (err == hipSuccess) return 0;
+    return SetError(static_cast<int>(err),
+                    std::string(what) + ": " + hipGetErrorName(err) + " (" +
+                        hipGetErrorString(err) + ")");
 }
 
 int CheckLaunch(const char* what, hipStream_t stream) {

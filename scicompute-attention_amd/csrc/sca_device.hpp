@@ -6,7 +6,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "sca_hip.h"
@@ -110,4 +112,25 @@ __device__ __forceinline__ void WaitVm() {
 namespace sca_hip {
 int SetError(int code, const std::string& message);
 int CheckLaunch(const char* what, hipStream_t stream);
+int FromHip(hipError_t err, const char* what);
+
+// Raises the dynamic LDS limit of kernel `Kernel` to `bytes` the first time it is launched in
+// the process. Safe to call from several threads; a failed attribute call is reported as an
+// error and retried on the next launch.
+template <auto Kernel>
+int EnsureLdsLimit(int bytes, const char* what) {
+    static std::atomic<bool> done{false};
+    static std::mutex mu;
+    if (done.load(std::memory_order_acquire)) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.load(std::memory_order_relaxed)) return 0;
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (err != hipSuccess) {
+        (void)hipGetLastError();
+        return FromHip(err, what);
+    }
+    done.store(true, std::memory_order_release);
+    return 0;
+}
 }  // namespace sca_hip

@@ -222,3 +222,14 @@ def test_c5_full_size_against_fp32(hip):
         w /= w.sum(axis=-1, keepdims=True)
         ref[s] = np.matmul(w, vs).reshape(Hq, D)
     check_attention(got.reshape(-1, D), ref.reshape(-1, D), "bf16", "paged C5 full size")
+
+
+@pytest.mark.parametrize("bs,L,splits", [(2, 9001, 2), (2, 9001, 3), (1, 5000, 1), (4, 20001, 2),
+                                         (16, 40000, 1)])
+@pytest.mark.parametrize("D,dtype", [(128, "bf16"), (96, "f16")])
+def test_splits_spanning_several_page_segments(hip, bs, L, splits, D, dtype):
+    """Splits longer than one staged page-id segment (2048 pages), starting on and off a page
+    boundary: the segment loop restages the page ids of every segment. D=128 bf16 runs the MFMA
+    kernel, D=96 the VALU kernel."""
+    print(f"paged multi-segment bs={bs} L={L} splits={splits} D={D} {dtype}", flush=True)
+    _case([L, 3], bs, 8, 2, D, dtype, 87000 + bs + splits + D, splits=splits)
