@@ -521,6 +521,121 @@ __device__ __forceinline__ float HalfSum(float v) {
     return lo + hi;
 }
 
+// ---- Online softmax of one 32-key x 32-row S^T tile (lane: 16 keys of one row; lanes l and
+// l ^ 32 hold the other 16 keys of the same row) -----------------------------------------------
+// Per-lane row state: the running max used for the exponentials (m, log2 units), the raw-score
+// threshold above which it must move (thr = (m + kRescaleSlack) / scale2), the exponent bias
+// (-m, or 0 while no key of the row was visible) and this lane's share of the denominator.
+struct RowState {
+    float m;
+    float thr;
+    float neg_mu;
+    float l;
+};
+
+__device__ __forceinline__ void ResetRow(RowState& r) {
+    r.m = neg_inf();
+    r.thr = neg_inf();
+    r.neg_mu = 0.0f;
+    r.l = 0.0f;
+}
+
+__device__ __forceinline__ float Max16(const floatx16& s) {
+    const float a = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    const float b = fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7]));
+    const float c = fmaxf(fmaxf(s[8], s[9]), fmaxf(s[10], s[11]));
+    const float d = fmaxf(fmaxf(s[12], s[13]), fmaxf(s[14], s[15]));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// Lazy rescale. The common case costs a local maximum and one compare: only when some lane of
+// the wave sees a score above its threshold does the wave exchange the two half-row maxima and
+// move m (to the row maximum, when it exceeds m by more than kRescaleSlack), scaling O and l by
+// 2^(m_old - m_new). The exponentials are then bounded by 2^kRescaleSlack.
+template <int DT>
+__device__ __forceinline__ void RescaleIfGrown(const floatx16& sv, float scale2, float inv_scale2,
+                                               RowState& r, floatx16 (&o)[DT]) {
+    const float lm = Max16(sv);
+    if (__builtin_amdgcn_ballot_w64(lm > r.thr) == 0) return;
+    const float tmax = HalfMax(lm) * scale2;
+    const bool grow = tmax > r.m + kRescaleSlack;
+    const float m_new = grow ? tmax : r.m;
+    const float alpha = grow ? fast_exp2(r.m - m_new) : 1.0f;  // 0 when m was -inf
+    r.m = m_new;
+    r.l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+    }
+    r.thr = (r.m + kRescaleSlack) * inv_scale2;
+    r.neg_mu = (r.m == neg_inf()) ? 0.0f : -r.m;
+}
+
+// P = 2^(s * scale2 - m) rounded to the input dtype as 8 packed pairs (the B operand of the PV
+// MFMAs), and the rounded weights added to the lane's denominator.
+template <typename M>
+__device__ __forceinline__ void ExpPack(const floatx16& sv, float scale2, RowState& r,
+                                        uint32_t (&pw)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float p0 = fast_exp2(fmaf(sv[2 * i], scale2, r.neg_mu));
+        const float p1 = fast_exp2(fmaf(sv[2 * i + 1], scale2, r.neg_mu));
+        pw[i] = M::pack(p0, p1);
+        r.l = M::sum2(pw[i], r.l);
+    }
+}
+
+// Transposed 8-byte LDS read at byte address addr + OFF. Issued from inline asm so that the
+// compiler's conservative LDS-DMA tracking adds no wait for DMAs still in flight; the caller
+// retires the reads with WaitLdsTied before the registers are used.
+template <int OFF>
+__device__ __forceinline__ uint2 TrReadAsm(uint32_t addr) {
+    uint2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+    return r;
+}
+
+// lgkmcnt(0), tied to the registers it guards so that no use of them is scheduled above it,
+// and to the P operands (a, b) so that it is not hoisted above the exponentials either.
+template <typename V, int N>
+__device__ __forceinline__ void WaitLdsTied(V (&regs)[N], V& a, V& b) {
+    if constexpr (N == 8) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(regs[0]), "+v"(regs[1]), "+v"(regs[2]), "+v"(regs[3]), "+v"(regs[4]),
+                       "+v"(regs[5]), "+v"(regs[6]), "+v"(regs[7]), "+v"(a), "+v"(b));
+    } else if constexpr (N == 4) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(regs[0]), "+v"(regs[1]), "+v"(regs[2]), "+v"(regs[3]), "+v"(a),
+                       "+v"(b));
+    } else {
+        static_assert(N == 8 || N == 4, "tied wait covers 4 or 8 registers");
+    }
+}
+
+__device__ __forceinline__ uint32_t LdsAddr(const void* p) {
+    return static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t*)(p)));
+}
+
+// V^T fragments of one key tile for the PV MFMAs: for O tile dt, k-step ps, the transposed
+// reads at rows 16*ps and 16*ps + 8 of the lane's V position (v_addr[dt], LDS byte address of
+// the slot-0 copy); SLOT_OFF selects the slot.
+template <int SLOT_OFF, int ROW_BYTES, int DT, typename vec8>
+__device__ __forceinline__ void ReadVFrags(const uint32_t (&v_addr)[DT], vec8 (&va)[2 * DT]) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+        const uint2 l0 = TrReadAsm<SLOT_OFF>(v_addr[dt]);
+        const uint2 h0 = TrReadAsm<SLOT_OFF + 8 * ROW_BYTES>(v_addr[dt]);
+        const uint2 l1 = TrReadAsm<SLOT_OFF + 16 * ROW_BYTES>(v_addr[dt]);
+        const uint2 h1 = TrReadAsm<SLOT_OFF + 24 * ROW_BYTES>(v_addr[dt]);
+        va[2 * dt] = __builtin_bit_cast(vec8, make_uint4(l0.x, l0.y, h0.x, h0.y));
+        va[2 * dt + 1] = __builtin_bit_cast(vec8, make_uint4(l1.x, l1.y, h1.x, h1.y));
+    }
+}
+
+constexpr int kSchedValuTrans = 0x402;  // VALU and transcendental
+
 // 16-byte DMA of lane data from a raw buffer (base, num_records) at voffset + soffset into LDS
 // at lds + 16 * lane. Bytes at or beyond num_records read as zero. (The buffer resource is
 // built here rather than in the kernel body: a buffer-resource local in a kernel body makes the
@@ -1141,6 +1256,7 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
     const int seq_kv = static_cast<int>(p.seq_kv);
     const int diag = static_cast<int>(p.diagonal);
     const float scale2 = p.scale * kLog2e;
+    const float inv_scale2 = 1.0f / scale2;
 
     const uint8_t* k_bytes = reinterpret_cast<const uint8_t*>(
         static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh);
@@ -1186,11 +1302,12 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
     const int v_key = wkey_base + 4 * hh + (sl >> 2);
     const int v_chunk = 2 * (grp & 1) + ((sl & 3) >> 1);
     const int v_half = (sl & 1) * 8;
-    uint32_t v_frag[G::DT];
+    uint32_t v_frag[G::DT], v_addr[G::DT];
 #pragma unroll
     for (int dt = 0; dt < G::DT; ++dt) {
         v_frag[dt] = g * G::RING_BYTES + v_key * ROW_BYTES +
                      (((4 * dt + v_chunk) ^ SwzV<D>(v_key)) * 16) + v_half;
+        v_addr[dt] = LdsAddr(lds8) + v_frag[dt];
     }
 
     // Row tiles: A = T-1-t (long), B = t (short; none when they coincide).
@@ -1235,15 +1352,14 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
     };
 
     floatx16 o[G::DT];
-    float m_used, l_run;
+    RowState rs;
     auto reset_state = [&]() {
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
         }
-        m_used = neg_inf();
-        l_run = 0.0f;
+        ResetRow(rs);
     };
 
     auto qk_slot = [&](int slot) {
@@ -1284,7 +1400,7 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
         }
     };
 
-    // Key tiles [kb, ke) of row tile qt into the running state (o, m_used, l_run).
+    // Key tiles [kb, ke) of row tile qt into the running state (o, rs.m, rs.l).
     auto run_keys = [&](int qt, int kb, int ke, int n_plain) {
         if (kb >= ke) return;
         const int my_q = qt * BM + rg * 32 + lr;
@@ -1306,9 +1422,25 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
         // then everything issued has landed before the group barrier. V's DMAs are issued
         // behind the K fragment reads of QK(j+1), so those start sooner (2-3% faster than
         // issuing both tiles first).
+        // Instruction order inside a step (each wave): V^T fragments of tile j and K fragments
+        // of tile j+1 are read first (nothing is in flight yet, so they start at once), then the
+        // step's DMAs go out; the masking and the local row maximum decide whether the rare
+        // rescale runs; the 8 QK MFMAs of tile j+1 are then interleaved one per 6 instructions
+        // of the exponentials of tile j, so the wave's VALU work issues while its MFMAs run;
+        // the PV MFMAs of tile j close the step. The QK of the last step reads a stale K slot
+        // (its result is unused), which keeps the step free of branches around the MFMAs.
         auto step = [&]<int S>(int j, floatx16& s_in, floatx16& s_out) {
+            vec8 va[2 * G::DT];
+            ReadVFrags<(2 + S) * G::TILE_BYTES, ROW_BYTES>(v_addr, va);
+            vec8 kf[G::KS];
+            {
+                const uint8_t* base = lds8 + (S ^ 1) * G::TILE_BYTES;
+#pragma unroll
+                for (int ks = 0; ks < G::KS; ++ks) {
+                    kf[ks] = *reinterpret_cast<const vec8*>(base + k_frag[ks]);
+                }
+            }
             if (j + 2 < ke) issue_k(j + 2);
-            if (j + 1 < ke) s_out = qk_slot(S ^ 1);
             if (j + 1 < ke) issue_v(j + 1);
             floatx16 sv = s_in;
             if (j >= n_plain) {
@@ -1320,42 +1452,30 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
                     sv[i] = key > lim ? neg_inf() : sv[i];
                 }
             }
-            float tmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                               fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-            tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(sv[8], sv[9]), fmaxf(sv[10], sv[11])),
-                                     fmaxf(fmaxf(sv[12], sv[13]), fmaxf(sv[14], sv[15]))));
-            tmax = HalfMax(tmax) * scale2;
-            const bool grow = tmax > m_used + kRescaleSlack;
-            const float m_new = grow ? tmax : m_used;
-            const float alpha = grow ? fast_exp2(m_used - m_new) : 1.0f;
-            m_used = m_new;
-            l_run *= alpha;
-            const float mu = (m_used == neg_inf()) ? 0.0f : m_used;
+            RescaleIfGrown(sv, scale2, inv_scale2, rs, o);
             uint32_t pw[8];
+            ExpPack<M>(sv, scale2, rs, pw);
+            floatx16 acc;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float p0 = fast_exp2(fmaf(sv[2 * i], scale2, -mu));
-                const float p1 = fast_exp2(fmaf(sv[2 * i + 1], scale2, -mu));
-                pw[i] = M::pack(p0, p1);
-                l_run = M::sum2(pw[i], l_run);
+            for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < G::KS; ++ks) acc = M::mma(kf[ks], qf[ks], acc);
+            s_out = acc;
+            vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+            vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
+            WaitLdsTied(va, pb0, pb1);
+#pragma unroll
+            for (int dt = 0; dt < G::DT; ++dt) {
+                o[dt] = M::mma(va[2 * dt], pb0, o[dt]);
+                o[dt] = M::mma(va[2 * dt + 1], pb1, o[dt]);
             }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(pw[i]));
-            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, G::KS / 2, 0);
 #pragma unroll
             for (int i = 0; i < G::KS; ++i) {
                 __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSchedValu, 10, 0);
-                if (i == 0) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, G::KS - G::KS / 2, 0);
+                __builtin_amdgcn_sched_group_barrier(kSchedValuTrans, 48 / G::KS, 0);
             }
-            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-#pragma unroll
-                for (int dt = 0; dt < G::DT; ++dt) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-                }
-            }
-            pv_slot(2 + S, pw);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * G::DT, 0);
+            __builtin_amdgcn_sched_barrier(0);
             WaitVm<0>();
             gsync();
         };
@@ -1397,15 +1517,15 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
                                         o[dt][4 * q4 + 3]);
                     }
                 }
-                bst[rg * kWave + lane] = make_float2(m_used, l_run);
+                bst[rg * kWave + lane] = make_float2(rs.m, rs.l);
             }
             gsync();
             if (kq == 0) {
                 const float2 st = bst[rg * kWave + lane];
-                const float mm = fmaxf(m_used, st.x);
-                const float w0 = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
+                const float mm = fmaxf(rs.m, st.x);
+                const float w0 = (rs.m == neg_inf()) ? 0.0f : fast_exp2(rs.m - mm);
                 const float w1 = (st.x == neg_inf()) ? 0.0f : fast_exp2(st.x - mm);
-                const float l_tot = HalfSum(l_run * w0 + st.y * w1);
+                const float l_tot = HalfSum(rs.l * w0 + st.y * w1);
                 const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
                 const int row = qb * BM + rg * 32 + lr;
                 const bool row_ok = row < seq_q;
@@ -1462,19 +1582,19 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
                                                           o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]);
             }
         }
-        mstat[(rg * 3 + src - 1) * kWave + lane] = make_float2(m_used, l_run);
+        mstat[(rg * 3 + src - 1) * kWave + lane] = make_float2(rs.m, rs.l);
     }
     __syncthreads();
     if (src == 0) {
         float2 st[3];
 #pragma unroll
         for (int q = 0; q < 3; ++q) st[q] = mstat[(rg * 3 + q) * kWave + lane];
-        float mm = m_used;
+        float mm = rs.m;
 #pragma unroll
         for (int q = 0; q < 3; ++q) mm = fmaxf(mm, st[q].x);
         float wq[4];
-        wq[0] = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
-        float l = l_run * wq[0];
+        wq[0] = (rs.m == neg_inf()) ? 0.0f : fast_exp2(rs.m - mm);
+        float l = rs.l * wq[0];
 #pragma unroll
         for (int q = 0; q < 3; ++q) {
             wq[q + 1] = (st[q].x == neg_inf()) ? 0.0f : fast_exp2(st[q].x - mm);
@@ -1518,6 +1638,717 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
                 l_tot > 0.0f ? (mm + __log2f(l_tot)) * kLn2 : neg_inf();
         }
     }
+}
+
+// ============================================================================================
+// Wide-row kernel (head_dim 64 and 128): one wave per SIMD and 64 query rows per wave.
+//
+// Why: the fragment reads from LDS are what bounds the 32-row kernels. Every K fragment (32 keys x
+// 16 dims) and every V^T fragment feeds one MFMA per 32 query rows a wave holds, and the
+// transposed V reads stream at about half the rate of ds_read_b128. With 64 rows per wave each
+// fragment feeds two MFMAs, which halves the LDS bytes per FLOP. 64 rows need about 250 VGPRs
+// plus 64 (D = 64) or 128 (D = 128) accumulator registers for O, which only one wave per SIMD
+// has; that wave then has to overlap its own VALU work with its MFMAs. It does when O lives in
+// AGPRs and the instruction stream alternates one MFMA with a few VALU instructions, so the
+// step below is written in an explicit order: every MFMA, fragment read and wait is an inline
+// asm statement, the C++ VALU code between them is fenced with sched_barrier, and the data
+// hazards the compiler cannot see are covered by waits stated at each use (see the step).
+//
+// Workgroup: 4 waves = 2 row groups (64 rows each, two 32-row subtiles) x 2 key halves (32 keys
+// of every 64-key tile); K and V tiles come by buffer->LDS DMA into rings of four slots each,
+// three tiles ahead. The two key halves of a row group are merged through LDS at the end.
+// ============================================================================================
+template <int D>
+struct WideGeom {
+    static constexpr int WAVES = 4;
+    static constexpr int THREADS = WAVES * kWave;
+    static constexpr int RT = 2;                      // 32-row subtiles per wave
+    static constexpr int BM = 128;                    // rows per workgroup
+    static constexpr int BN = 64;                     // keys per tile
+    static constexpr int KS = D / 16;                 // QK k-steps
+    static constexpr int DT = D / 32;                 // O^T tiles of 32 dims
+    static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+    static constexpr int ROW_BYTES = 2 * D;
+    static constexpr int TILE_BYTES = BN * ROW_BYTES;
+    static constexpr int IPW = BN * CPR / (kWave * WAVES);  // DMA instructions per wave per tile
+    static constexpr int SLOTS = 4;
+    static constexpr int V_BASE = SLOTS * TILE_BYTES;
+    static constexpr int RING_BYTES = 2 * SLOTS * TILE_BYTES;
+    // Merge: the two kq = 1 waves' O (RT*DT*16 floats per lane) and (m, l) per subtile.
+    static constexpr int MERGE_FLOATS = RT * DT * 16 + 2 * RT;
+    static constexpr int MERGE_BYTES = 2 * kWave * MERGE_FLOATS * 4;
+    static constexpr int LDS_BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
+    static_assert(IPW >= 1 && BN * CPR == IPW * kWave * WAVES, "tile must split evenly");
+    static_assert((SLOTS - 1) * TILE_BYTES + 24 * ROW_BYTES < 65536, "slot offsets are DS immediates");
+};
+
+// MFMAs issued from inline asm: S^T accumulators in VGPRs, O^T accumulators in AGPRs.
+template <typename E>
+struct MfmaAsm;
+
+template <>
+struct MfmaAsm<F16> {
+    // S^T: A (K fragment) in VGPRs, B (Q fragment) in AGPRs, accumulator in VGPRs.
+    template <typename V>
+    static __device__ __forceinline__ void first_v(floatx16& c, const V& a, const V& b) {
+        asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "a"(b));
+    }
+    template <typename V>
+    static __device__ __forceinline__ void acc_v(floatx16& c, const V& a, const V& b) {
+        asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "a"(b));
+    }
+    template <typename V>
+    static __device__ __forceinline__ void acc_a(floatx16& c, const V& a, const V& b) {
+        asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    }
+};
+
+template <>
+struct MfmaAsm<BF16> {
+    // S^T: A (K fragment) in VGPRs, B (Q fragment) in AGPRs, accumulator in VGPRs.
+    template <typename V>
+    static __device__ __forceinline__ void first_v(floatx16& c, const V& a, const V& b) {
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "a"(b));
+    }
+    template <typename V>
+    static __device__ __forceinline__ void acc_v(floatx16& c, const V& a, const V& b) {
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "a"(b));
+    }
+    template <typename V>
+    static __device__ __forceinline__ void acc_a(floatx16& c, const V& a, const V& b) {
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    }
+};
+
+template <int OFF, typename V>
+__device__ __forceinline__ void ReadB128Asm(V& dst, uint32_t addr) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(OFF));
+}
+
+// lgkmcnt(N) tied to the register it guards (the asm uses below it cannot move above it).
+template <int N, typename V>
+__device__ __forceinline__ void WaitLgkmTied(V& reg) {
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(reg) : "i"(N));
+}
+
+__device__ __forceinline__ void Fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Ablation mask of the wide kernel's step (measurement builds only; 0 in the shipped library):
+// 1 no PV MFMAs, 2 no QK MFMAs, 4 no exponentials, 8 no V reads, 16 no K reads, 32 no DMAs,
+// 64 no barrier. The results of an ablated build are wrong by construction.
+#if defined(SCA_MEASUREMENT_BUILD) && defined(SCA_ABL)
+constexpr int kAbl = SCA_ABL;
+#else
+constexpr int kAbl = 0;
+#endif
+
+// Region clocks of the wide kernel's steps (measurement builds with SCA_STAMPS only): per wave,
+// the shader cycles spent in each of 8 regions summed over the steps, read back through
+// sca_hip_debug_wide_stamps.
+#if defined(SCA_MEASUREMENT_BUILD) && defined(SCA_STAMPS)
+constexpr bool kStamps = true;
+__device__ uint32_t g_wide_stamps[4096 * 4][9];
+#else
+constexpr bool kStamps = false;
+#endif
+// Issues s_memtime without waiting for it: the value may be read only after an lgkmcnt(0).
+__device__ __forceinline__ uint64_t MemtimeNoWait() {
+    uint64_t v;
+    asm volatile("s_memtime %0" : "=s"(v));
+    return v;
+}
+
+// Gives a value the AGPR register class (an empty asm with an AGPR in/out operand), so that the
+// loop-carried accumulators and Q fragments stay in AGPRs instead of being copied in and out.
+template <typename V>
+__device__ __forceinline__ void PinAgpr(V& x) {
+    asm volatile("" : "+a"(x));
+}
+
+// 32 wait states tied to the O accumulators (AGPRs): VALU access to O placed after this waits
+// for the last MFMA that wrote O, which the compiler does not track for inline-asm MFMAs.
+template <int DT>
+__device__ __forceinline__ void SettleO(floatx16 (&o)[2][DT]) {
+    if constexpr (DT == 4) {
+        asm volatile("s_nop 15\n\ts_nop 15"
+                     : "+a"(o[0][0]), "+a"(o[0][1]), "+a"(o[0][2]), "+a"(o[0][3]), "+a"(o[1][0]),
+                       "+a"(o[1][1]), "+a"(o[1][2]), "+a"(o[1][3]));
+    } else {
+        static_assert(DT == 2, "head_dim 64 or 128");
+        asm volatile("s_nop 15\n\ts_nop 15" : "+a"(o[0][0]), "+a"(o[0][1]), "+a"(o[1][0]), "+a"(o[1][1]));
+    }
+}
+
+template <typename E, int D, bool kCausal>
+__global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel(
+    const sca_flash_params p, int num_q_tiles) {
+    using G = WideGeom<D>;
+    using M = Mfma<E>;
+    using A = MfmaAsm<E>;
+    using vec8 = typename E::vec8;
+    constexpr int BN = G::BN;
+    constexpr int BM = G::BM;
+    constexpr int RB = G::ROW_BYTES;
+
+    extern __shared__ __align__(16) uint8_t lds8[];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int lane = tid % kWave;
+    const int lr = lane & 31;
+    const int hh = lane >> 5;
+    const int rg = wave & 1;   // row group: rows 64*rg .. +64 of the row tile
+    const int kq = wave >> 1;  // key half: keys 32*kq .. +32 of every key tile
+
+    const int64_t bh_count = p.batch * p.num_heads;
+    const int64_t tile_linear = static_cast<int64_t>(blockIdx.x) / bh_count;
+    const int64_t bh = static_cast<int64_t>(blockIdx.x) % bh_count;
+    const int64_t b = bh / p.num_heads;
+    const int64_t h = bh % p.num_heads;
+    const int64_t h_kv = h / (p.num_heads / p.num_kv_heads);
+    // Causal: longest row tiles first.
+    const int qt = static_cast<int>(kCausal ? (num_q_tiles - 1 - tile_linear) : tile_linear);
+    const int seq_q = static_cast<int>(p.seq_q);
+    const int seq_kv = static_cast<int>(p.seq_kv);
+    const int diag = static_cast<int>(p.diagonal);
+    const float scale2 = p.scale * kLog2e;
+    const float inv_scale2 = 1.0f / scale2;
+    const int q0 = qt * BM;
+    const int row0 = q0 + 64 * rg + lr;  // row of subtile 0 (subtile 1: +32)
+
+    int n_tiles = (seq_kv + BN - 1) / BN;
+    int n_plain = seq_kv / BN;
+    if (kCausal) {
+        const int last_key = q0 + BM - 1 + diag;
+        const int causal_tiles = last_key < 0 ? 0 : last_key / BN + 1;
+        if (causal_tiles < n_tiles) n_tiles = causal_tiles;
+        const int plain = (q0 + diag + 1) / BN;
+        if (plain < n_plain) n_plain = plain;
+    }
+    if (n_plain > n_tiles) n_plain = n_tiles;
+
+    // ---- Q fragments (B operand of S^T = K Q^T): subtile r, k-step ks ----
+    vec8 qf[G::RT][G::KS];
+#pragma unroll
+    for (int r = 0; r < G::RT; ++r) {
+        const int row = row0 + 32 * r;
+        const uint16_t* q_row = static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh +
+                                static_cast<int64_t>(row) * p.q_ss + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+            uint4 raw = make_uint4(0, 0, 0, 0);
+            if (row < seq_q) raw = *reinterpret_cast<const uint4*>(q_row + 16 * ks);
+            qf[r][ks] = __builtin_bit_cast(vec8, raw);
+        }
+    }
+
+    // ---- DMA (as in the DMA kernel: buffer resources bounded at the last row) ----
+    const uint8_t* k_bytes = reinterpret_cast<const uint8_t*>(
+        static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh);
+    const uint8_t* v_bytes = reinterpret_cast<const uint8_t*>(
+        static_cast<const uint16_t*>(p.v) + b * p.v_sb + h_kv * p.v_sh);
+    const int k_row_bytes = static_cast<int>(p.k_ss) * 2;
+    const int v_row_bytes = static_cast<int>(p.v_ss) * 2;
+    const int k_records = (seq_kv - 1) * k_row_bytes + RB;
+    const int v_records = (seq_kv - 1) * v_row_bytes + RB;
+    uint32_t dma_koff[G::IPW], dma_voff[G::IPW];
+#pragma unroll
+    for (int i = 0; i < G::IPW; ++i) {
+        const int P = (wave * G::IPW + i) * kWave + lane;
+        const int row = P / G::CPR;
+        const int pos = P % G::CPR;
+        dma_koff[i] = row * k_row_bytes + (pos ^ SwzK<D>(row)) * 16;
+        dma_voff[i] = row * v_row_bytes + (pos ^ SwzV<D>(row)) * 16;
+    }
+    auto issue_k = [&](int slot, int t) __attribute__((always_inline)) {
+        uint8_t* dst = lds8 + slot * G::TILE_BYTES + wave * G::IPW * 1024;
+        const uint32_t off = static_cast<uint32_t>(t * BN * k_row_bytes);
+#pragma unroll
+        for (int i = 0; i < G::IPW; ++i) DmaToLds(k_bytes, k_records, dst + i * 1024, dma_koff[i], off);
+    };
+    auto issue_v = [&](int slot, int t) __attribute__((always_inline)) {
+        uint8_t* dst = lds8 + G::V_BASE + slot * G::TILE_BYTES + wave * G::IPW * 1024;
+        const uint32_t off = static_cast<uint32_t>(t * BN * v_row_bytes);
+#pragma unroll
+        for (int i = 0; i < G::IPW; ++i) DmaToLds(v_bytes, v_records, dst + i * 1024, dma_voff[i], off);
+    };
+    // DMA instruction n (of 2*IPW: K's then V's) of the step that fetches K(t + 1) and V(t).
+    auto issue_one = [&](int n, int k_slot, int v_slot, int t_k, int t_v) __attribute__((always_inline)) {
+        if (n < G::IPW) {
+            uint8_t* dst = lds8 + k_slot * G::TILE_BYTES + wave * G::IPW * 1024;
+            DmaToLds(k_bytes, k_records, dst + n * 1024, dma_koff[n],
+                     static_cast<uint32_t>(t_k * BN * k_row_bytes));
+        } else {
+            const int i = n - G::IPW;
+            uint8_t* dst = lds8 + G::V_BASE + v_slot * G::TILE_BYTES + wave * G::IPW * 1024;
+            DmaToLds(v_bytes, v_records, dst + i * 1024, dma_voff[i],
+                     static_cast<uint32_t>(t_v * BN * v_row_bytes));
+        }
+    };
+
+    // ---- fragment addresses (LDS byte addresses of slot 0; slots are immediate offsets) ----
+    const uint32_t lds_base = LdsAddr(lds8);
+    const int k_row = 32 * kq + lr;
+    uint32_t k_addr[G::KS];
+#pragma unroll
+    for (int ks = 0; ks < G::KS; ++ks) {
+        k_addr[ks] = lds_base + k_row * RB + (((2 * ks) ^ hh ^ SwzK<D>(k_row)) * 16);
+    }
+    const int grp = lane >> 4;
+    const int sl = lane & 15;
+    const int v_key = 32 * kq + 4 * hh + (sl >> 2);
+    const int v_chunk = 2 * (grp & 1) + ((sl & 3) >> 1);
+    const int v_half = (sl & 1) * 8;
+    uint32_t v_addr[G::DT];
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt) {
+        v_addr[dt] = lds_base + G::V_BASE + v_key * RB +
+                     (((4 * dt + v_chunk) ^ SwzV<D>(v_key)) * 16) + v_half;
+    }
+
+    floatx16 o[G::RT][G::DT];
+#pragma unroll
+    for (int r = 0; r < G::RT; ++r) {
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[r][dt][i] = 0.0f;
+            PinAgpr(o[r][dt]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < G::RT; ++r) {
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) PinAgpr(qf[r][ks]);
+    }
+    // Row state (RowState); the denominator is summed in two halves (rs.l and l2), which keeps
+    // the two dependency chains of its additions apart.
+    RowState rs[G::RT];
+    float l2[G::RT];
+#pragma unroll
+    for (int r = 0; r < G::RT; ++r) {
+        ResetRow(rs[r]);
+        l2[r] = 0.0f;
+    }
+
+    // K fragments of the next key tile, and two V^T fragment buffers (tile parity).
+    vec8 kf[G::KS];
+    vec8 va[2][2 * G::DT];
+    auto read_k = [&]<int SLOT>() __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) ReadB128Asm<SLOT * G::TILE_BYTES>(kf[ks], k_addr[ks]);
+    };
+    // Transposed V read i (of 4*DT) of the V tile in slot SLOT into buffer VB.
+    auto read_v1 = [&]<int SLOT, int VB>(int i) __attribute__((always_inline)) {
+        const int dt = i / 4;
+        const int part = i % 4;
+        uint2 r;
+        switch (part) {
+            case 0: r = TrReadAsm<SLOT * G::TILE_BYTES>(v_addr[dt]); break;
+            case 1: r = TrReadAsm<SLOT * G::TILE_BYTES + 8 * RB>(v_addr[dt]); break;
+            case 2: r = TrReadAsm<SLOT * G::TILE_BYTES + 16 * RB>(v_addr[dt]); break;
+            default: r = TrReadAsm<SLOT * G::TILE_BYTES + 24 * RB>(v_addr[dt]); break;
+        }
+        // fragment 2*dt + ps holds (rows 16*ps, 16*ps + 8) of the lane's V column
+        uint4 w = __builtin_bit_cast(uint4, va[VB][2 * dt + part / 2]);
+        if (part % 2 == 0) {
+            w.x = r.x;
+            w.y = r.y;
+        } else {
+            w.z = r.x;
+            w.w = r.y;
+        }
+        va[VB][2 * dt + part / 2] = __builtin_bit_cast(vec8, w);
+    };
+
+    // Masking of S^T subtile r of key tile t (uniform `masked`), and the lane's local maximum.
+    auto mask_max = [&](floatx16& sr, int r, int t, bool masked) __attribute__((always_inline)) -> float {
+        if (masked) {
+            const int kbase = t * BN + 32 * kq + 4 * hh;
+            const int lim = kCausal ? min(seq_kv - 1, row0 + 32 * r + diag) : seq_kv - 1;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kbase + 8 * (i / 4) + (i % 4);
+                sr[i] = key > lim ? neg_inf() : sr[i];
+            }
+        }
+        return Max16(sr);
+    };
+    // The rare rescale of both subtiles for a new key tile with raw lane maxima lm (RowState).
+    auto rescale_if_grown = [&](float lm0, float lm1) __attribute__((always_inline)) {
+        if (__builtin_amdgcn_ballot_w64((lm0 > rs[0].thr) || (lm1 > rs[1].thr)) == 0) return;
+        SettleO(o);
+        const float lmv[2] = {lm0, lm1};
+#pragma unroll
+        for (int r = 0; r < G::RT; ++r) {
+            const float cmax = HalfMax(lmv[r]) * scale2;  // row maximum, log2 units
+            const bool grow = cmax > rs[r].m + kRescaleSlack;
+            const float m_new = grow ? cmax : rs[r].m;
+            const float alpha = grow ? fast_exp2(rs[r].m - m_new) : 1.0f;  // 0 when m was -inf
+            rs[r].m = m_new;
+            rs[r].l *= alpha;
+            l2[r] *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < G::DT; ++dt) {
+                Fence();  // one O tile at a time through VGPRs
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[r][dt][i] *= alpha;
+                PinAgpr(o[r][dt]);
+            }
+            Fence();
+            rs[r].thr = (m_new + kRescaleSlack) * inv_scale2;
+            rs[r].neg_mu = (m_new == neg_inf()) ? 0.0f : -m_new;
+        }
+        asm volatile("s_nop 4");
+    };
+
+    // ---- prologue: K(0..3), V(0..2) in flight; S(0), its maxima and rescale; K(1) and V(0)
+    //      fragments read for step 0; K(2) and V(1) landed before step 0 ----
+    issue_k(0, 0);
+    issue_k(1, 1);
+    issue_v(0, 0);
+    issue_k(2, 2);
+    issue_v(1, 1);
+    issue_k(3, 3);
+    issue_v(2, 2);
+    WaitVm<4 * G::IPW>();  // K(0), K(1), V(0)
+    __builtin_amdgcn_s_barrier();
+    floatx16 s0[G::RT], s1[G::RT];
+    read_k.template operator()<0>();
+    WaitLgkmTied<0>(kf[0]);
+#pragma unroll
+    for (int ks = 1; ks < G::KS; ++ks) WaitLgkmTied<0>(kf[ks]);
+#pragma unroll
+    for (int r = 0; r < G::RT; ++r) {
+        A::first_v(s0[r], kf[0], qf[r][0]);
+#pragma unroll
+        for (int ks = 1; ks < G::KS; ++ks) A::acc_v(s0[r], kf[ks], qf[r][ks]);
+    }
+    asm volatile("s_nop 15\n\ts_nop 15");  // the QK results are complete; kf has been read
+    {
+        const float lm0 = mask_max(s0[0], 0, 0, n_plain == 0);
+        const float lm1 = mask_max(s0[1], 1, 0, n_plain == 0);
+        rescale_if_grown(lm0, lm1);
+    }
+    read_k.template operator()<1>();
+#pragma unroll
+    for (int i = 0; i < 4 * G::DT; ++i) read_v1.template operator()<0, 0>(i);
+    WaitVm<2 * G::IPW>();  // K(2), V(1)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+
+    uint32_t st_acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint64_t st_t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint64_t st_prev = 0;
+
+    // One step for key tile j (S = j & 3, VB = j & 1). On entry S(j) is masked and the rescale
+    // for tile j is done, kf holds K(j+1)'s fragments and va[VB] V(j)'s. Four regions, each one
+    // MFMA stream with VALU and LDS work placed between its MFMAs:
+    //   A  QK(j+1) of subtile 0          | the 8 exponential pairs of S(j) subtile 0
+    //   B  PV(j) of subtile 0            | exponential pairs 0-3 of subtile 1, V(j+1)'s reads
+    //   C  QK(j+1) of subtile 1          | exponential pairs 4-7 of subtile 1, S(j+1) subtile 0's
+    //                                      masking and maximum
+    //   D  PV(j) of subtile 1            | S(j+1) subtile 1's masking and maximum, K(j+2)'s
+    //                                      fragment reads, the DMAs of K(j+4) and V(j+3)
+    // then the rare rescale for tile j+1, the DMA wait (K(j+3) and V(j+2) must land: only the
+    // two groups issued in this step stay in flight) and the barrier. Hazards the compiler
+    // does not see (inline-asm MFMAs): a QK result is read by VALU only after at least two
+    // later MFMAs and 5 wait states; kf is rewritten only after two later MFMAs; the O
+    // accumulators are read by VALU only through SettleO; P operands are written by VALU at
+    // least a region before their MFMAs.
+    auto step = [&]<bool kMaskable, int S>(int j, floatx16 (&s_in)[G::RT],
+                                           floatx16 (&s_out)[G::RT]) __attribute__((always_inline)) {
+        constexpr int VB = S & 1;
+        constexpr int NPV = 2 * G::DT;  // PV MFMAs per subtile
+        if constexpr (kStamps) st_t[0] = MemtimeNoWait();
+        const bool next_ok = !kMaskable || j + 1 < n_tiles;   // S(j+1) is a real tile
+        const bool next_masked = kMaskable && j + 1 >= n_plain;
+        uint32_t pw[G::RT][8];
+        // The 56 VALU operations that turn S(j) subtile r into P: 16 exponent arguments
+        // s * scale2 - m (codes 0-15), 16 exponentials (16-31), 8 packs to the input dtype
+        // (32-39) and 16 additions of the fp32 weights into the two denominator halves (40-55),
+        // all in place; op(r, n) runs the n-th in the order of kOps, which keeps each result at
+        // least two operations from its first use. (The sums use v_add: a v_dot2 issued between
+        // MFMAs does not overlap with them.)
+        auto op = [&](int r, int n) __attribute__((always_inline)) {
+            constexpr int kOps[56] = {0,  1,  2,  3,  16, 17, 4,  5,  18, 19, 6,  7,  20, 21,
+                                      32, 33, 8,  9,  22, 23, 34, 10, 11, 24, 25, 35, 40, 41,
+                                      12, 13, 26, 27, 36, 42, 43, 14, 15, 28, 29, 37, 44, 45,
+                                      30, 31, 46, 47, 38, 39, 48, 49, 50, 51, 52, 53, 54, 55};
+            const int c = kOps[n];
+            if (kAbl & 4) {
+                if (c >= 32 && c < 40) pw[r][c - 32] = 0x3c003c00u;
+                return;
+            }
+            if (c < 16) {
+                s_in[r][c] = fmaf(s_in[r][c], scale2, rs[r].neg_mu);
+            } else if (c < 32) {
+                s_in[r][c - 16] = fast_exp2(s_in[r][c - 16]);
+            } else if (c < 40) {
+                pw[r][c - 32] = M::pack(s_in[r][2 * (c - 32)], s_in[r][2 * (c - 32) + 1]);
+            } else if (c % 2 == 0) {
+                rs[r].l += s_in[r][c - 40];
+            } else {
+                l2[r] += s_in[r][c - 40];
+            }
+        };
+        auto qk = [&](int r, int ks) __attribute__((always_inline)) {
+            if (kAbl & 2) return;
+            if (ks == 0) {
+                A::first_v(s_out[r], kf[0], qf[r][0]);
+            } else {
+                A::acc_v(s_out[r], kf[ks], qf[r][ks]);
+            }
+        };
+        vec8 pb[G::RT][2];
+        auto pack_p = [&](int r) __attribute__((always_inline)) {
+            pb[r][0] = __builtin_bit_cast(vec8, make_uint4(pw[r][0], pw[r][1], pw[r][2], pw[r][3]));
+            pb[r][1] = __builtin_bit_cast(vec8, make_uint4(pw[r][4], pw[r][5], pw[r][6], pw[r][7]));
+        };
+        auto pv = [&](int r, int i) __attribute__((always_inline)) {
+            if (kAbl & 1) return;
+            A::acc_a(o[r][i / 2], va[VB][i], pb[r][i % 2]);
+        };
+        // The step's 2*IPW DMA instructions (K(j+4) into K slot S, V(j+3) into V slot S-1),
+        // spread over the four regions: in region g, after MFMA i, instruction number
+        // g*kDmaPerRegion + i / kDmaSpacing when i is a multiple of kDmaSpacing.
+        constexpr int kDmaPerRegion = (2 * G::IPW + 3) / 4;
+        auto dma = [&](int g, int i) __attribute__((always_inline)) {
+            if (kAbl & 32) return;
+            constexpr int kSpacing = 8 / kDmaPerRegion > 0 ? 8 / kDmaPerRegion : 1;
+            if (i % kSpacing != 0) return;
+            const int n = g * kDmaPerRegion + i / kSpacing;
+            if (n >= 2 * G::IPW || i / kSpacing >= kDmaPerRegion) return;
+            const bool is_k = n < G::IPW;
+            if (kMaskable && (is_k ? j + 4 >= n_tiles : j + 3 >= n_tiles)) return;
+            issue_one(n, S, (S + 3) & 3, j + 4, j + 3);
+        };
+
+        // ---- A ----
+        constexpr int kOpsA = 56 / G::KS;  // VALU operations per QK MFMA
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+            qk(0, ks);
+            Fence();
+#pragma unroll
+            for (int q = 0; q < kOpsA; ++q) op(0, ks * kOpsA + q);
+            dma(0, ks);
+            Fence();
+        }
+        pack_p(0);
+        // P operands: 2 wait states after their VALU writes (the compiler does not see the
+        // inline-asm MFMA that reads them).
+        asm volatile("s_nop 1" : "+v"(pb[0][0]), "+v"(pb[0][1]));
+        if constexpr (kStamps) st_t[1] = MemtimeNoWait();
+        // ---- B ----
+        constexpr int kVReadsB = 4 * G::DT / NPV;  // V reads per PV MFMA
+        constexpr int kOpsB = (28 + NPV - 1) / NPV;  // subtile 1's operations 0-27
+#pragma unroll
+        for (int i = 0; i < NPV; ++i) {
+            pv(0, i);
+            Fence();
+#pragma unroll
+            for (int q = 0; q < kOpsB; ++q) {
+                if (i * kOpsB + q < 28) op(1, i * kOpsB + q);
+            }
+            dma(1, i);
+            if (!(kAbl & 8)) {
+#pragma unroll
+                for (int q = 0; q < kVReadsB; ++q) {
+                    read_v1.template operator()<(S + 1) & 3, VB ^ 1>(i * kVReadsB + q);
+                }
+            }
+            Fence();
+        }
+        if constexpr (kStamps) st_t[2] = MemtimeNoWait();
+        // ---- C ----
+        float lm0 = neg_inf(), lm1 = neg_inf();
+        constexpr int kOpsC = (28 + G::KS - 1) / G::KS;  // subtile 1's operations 28-55
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+            qk(1, ks);
+            Fence();
+#pragma unroll
+            for (int q = 0; q < kOpsC; ++q) {
+                if (ks * kOpsC + q < 28) op(1, 28 + ks * kOpsC + q);
+            }
+            dma(2, ks);
+            if (ks == G::KS / 2) {
+                if (next_ok) lm0 = mask_max(s_out[0], 0, j + 1, next_masked);
+            }
+            Fence();
+        }
+        pack_p(1);
+        // P operands: 2 wait states after their VALU writes.
+        asm volatile("s_nop 1" : "+v"(pb[1][0]), "+v"(pb[1][1]));
+        if constexpr (kStamps) st_t[3] = MemtimeNoWait();
+        // ---- D ----
+#pragma unroll
+        for (int i = 0; i < NPV; ++i) {
+            pv(1, i);
+            Fence();
+            if (i == 1) {
+                asm volatile("s_nop 4");
+                if (next_ok) lm1 = mask_max(s_out[1], 1, j + 1, next_masked);
+            }
+            if (i >= 1 && !(kAbl & 16)) {
+                // KS K reads over the MFMAs 1 .. NPV-1 (kf was last read two MFMAs ago).
+                constexpr int kPer = (G::KS + NPV - 2) / (NPV - 1);
+#pragma unroll
+                for (int q = 0; q < kPer; ++q) {
+                    const int ks = (i - 1) * kPer + q;
+                    if (ks < G::KS) {
+                        switch (ks) {
+                            case 0: ReadB128Asm<((S + 2) & 3) * G::TILE_BYTES>(kf[0], k_addr[0]); break;
+                            case 1: ReadB128Asm<((S + 2) & 3) * G::TILE_BYTES>(kf[1], k_addr[1]); break;
+                            case 2: ReadB128Asm<((S + 2) & 3) * G::TILE_BYTES>(kf[2], k_addr[2]); break;
+                            case 3: ReadB128Asm<((S + 2) & 3) * G::TILE_BYTES>(kf[3], k_addr[3]); break;
+                            case 4: ReadB128Asm<((S + 2) & 3) * G::TILE_BYTES>(kf[4 % G::KS], k_addr[4 % G::KS]); break;
+                            case 5: ReadB128Asm<((S + 2) & 3) * G::TILE_BYTES>(kf[5 % G::KS], k_addr[5 % G::KS]); break;
+                            case 6: ReadB128Asm<((S + 2) & 3) * G::TILE_BYTES>(kf[6 % G::KS], k_addr[6 % G::KS]); break;
+                            default: ReadB128Asm<((S + 2) & 3) * G::TILE_BYTES>(kf[7 % G::KS], k_addr[7 % G::KS]); break;
+                        }
+                    }
+                }
+            }
+            dma(3, i);
+            Fence();
+        }
+        if constexpr (kStamps) st_t[4] = MemtimeNoWait();
+        // ---- rare rescale for tile j+1 ----
+        if (next_ok) rescale_if_grown(lm0, lm1);
+        Fence();
+        if constexpr (kStamps) st_t[5] = MemtimeNoWait();
+        // ---- K(j+3) and V(j+2) landed (at the tail, everything); fragment reads retired ----
+        if (!kMaskable || j + 4 < n_tiles) {
+            WaitVm<2 * G::IPW>();
+        } else {
+            WaitVm<0>();
+        }
+        WaitLgkmTied<0>(kf[G::KS - 1]);
+        if constexpr (kStamps) {
+            st_t[6] = MemtimeNoWait();
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (st_prev != 0) st_acc[7] += static_cast<uint32_t>(st_t[0] - st_prev);
+            for (int k = 0; k < 6; ++k) st_acc[k] += static_cast<uint32_t>(st_t[k + 1] - st_t[k]);
+            st_prev = st_t[6];
+        }
+        if (!(kAbl & 64)) __builtin_amdgcn_s_barrier();
+    };
+
+    int j = 0;
+    // Steady state: plain tiles with the full ring ahead, four steps per trip.
+    for (; j + 5 <= n_plain && j + 8 <= n_tiles; j += 4) {
+        step.template operator()<false, 0>(j, s0, s1);
+        step.template operator()<false, 1>(j + 1, s1, s0);
+        step.template operator()<false, 2>(j + 2, s0, s1);
+        step.template operator()<false, 3>(j + 3, s1, s0);
+    }
+    // Tail (j is a multiple of 4 here): masked steps, same slot rotation.
+    for (; j < n_tiles; j += 4) {
+        step.template operator()<true, 0>(j, s0, s1);
+        if (j + 1 >= n_tiles) break;
+        step.template operator()<true, 1>(j + 1, s1, s0);
+        if (j + 2 >= n_tiles) break;
+        step.template operator()<true, 2>(j + 2, s0, s1);
+        if (j + 3 >= n_tiles) break;
+        step.template operator()<true, 3>(j + 3, s1, s0);
+    }
+
+#if defined(SCA_MEASUREMENT_BUILD) && defined(SCA_STAMPS)
+    if (lane == 0 && blockIdx.x < 4096) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) g_wide_stamps[blockIdx.x * 4 + wave][k] = st_acc[k];
+        g_wide_stamps[blockIdx.x * 4 + wave][8] = static_cast<uint32_t>(n_tiles);
+    }
+#endif
+    // ---- epilogue: merge the key halves of each row group, normalise, store ----
+    WaitVm<0>();
+    SettleO(o);
+    __builtin_amdgcn_s_barrier();
+    float* const mbuf = reinterpret_cast<float*>(lds8) + rg * kWave * G::MERGE_FLOATS;
+    if (kq == 1) {
+        // O as quads, quad k of lane L at k*64 + L (conflict-free 16-byte accesses).
+        float4* q4 = reinterpret_cast<float4*>(mbuf) + lane;
+#pragma unroll
+        for (int r = 0; r < G::RT; ++r) {
+#pragma unroll
+            for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    q4[((r * G::DT + dt) * 4 + g) * kWave] =
+                        make_float4(o[r][dt][4 * g], o[r][dt][4 * g + 1], o[r][dt][4 * g + 2],
+                                    o[r][dt][4 * g + 3]);
+                }
+            }
+        }
+        float2* st = reinterpret_cast<float2*>(mbuf + G::RT * G::DT * 16 * kWave) + lane;
+#pragma unroll
+        for (int r = 0; r < G::RT; ++r) st[r * kWave] = make_float2(rs[r].m, rs[r].l + l2[r]);
+    }
+    __syncthreads();
+    if (kq == 1) return;
+
+    const float4* q4 = reinterpret_cast<const float4*>(mbuf) + lane;
+    const float2* st = reinterpret_cast<const float2*>(mbuf + G::RT * G::DT * 16 * kWave) + lane;
+#pragma unroll
+    for (int r = 0; r < G::RT; ++r) {
+        const float2 other = st[r * kWave];
+        const float mm = fmaxf(rs[r].m, other.x);
+        const float w0 = (rs[r].m == neg_inf()) ? 0.0f : fast_exp2(rs[r].m - mm);
+        const float w1 = (other.x == neg_inf()) ? 0.0f : fast_exp2(other.x - mm);
+        const float l_tot = HalfSum((rs[r].l + l2[r]) * w0) + HalfSum(other.y * w1);
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        const int row = row0 + 32 * r;
+        const bool row_ok = row < seq_q;
+        uint16_t* out_row = static_cast<uint16_t*>(p.out) + b * p.o_sb + h * p.o_sh +
+                            static_cast<int64_t>(row) * p.o_ss;
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 v = q4[((r * G::DT + dt) * 4 + g) * kWave];
+                const float a0 = (o[r][dt][4 * g] * w0 + v.x * w1) * inv;
+                const float a1 = (o[r][dt][4 * g + 1] * w0 + v.y * w1) * inv;
+                const float a2 = (o[r][dt][4 * g + 2] * w0 + v.z * w1) * inv;
+                const float a3 = (o[r][dt][4 * g + 3] * w0 + v.w * w1) * inv;
+                if (row_ok) {
+                    const int d0 = 32 * dt + 8 * g + 4 * hh;
+                    *reinterpret_cast<uint2*>(out_row + d0) =
+                        make_uint2(M::pack(a0, a1), M::pack(a2, a3));
+                }
+            }
+        }
+        if (row_ok && p.lse != nullptr && hh == 0) {
+            p.lse[(b * p.num_heads + h) * p.seq_q + row] =
+                l_tot > 0.0f ? (mm + __log2f(l_tot)) * kLn2 : neg_inf();
+        }
+    }
+}
+
+template <typename E, int D, bool kCausal>
+int LaunchFlash(const sca_flash_params& p, hipStream_t s);
+
+template <typename E, int D, bool kCausal>
+int LaunchFlashWide(const sca_flash_params& p, hipStream_t s) {
+    using G = WideGeom<D>;
+    // Buffer offsets are 32-bit: rows up to seq_kv plus the ring's overrun must fit.
+    const int64_t extent_k = (p.seq_kv + 8 * G::BN) * p.k_ss * 2;
+    const int64_t extent_v = (p.seq_kv + 8 * G::BN) * p.v_ss * 2;
+    if (extent_k >= (1LL << 31) || extent_v >= (1LL << 31)) return LaunchFlash<E, D, kCausal>(p, s);
+    const int64_t num_q_tiles = (p.seq_q + G::BM - 1) / G::BM;
+    const int64_t blocks = num_q_tiles * p.batch * p.num_heads;
+    if (blocks <= 0) return 0;
+    if (blocks > 0x7fffffffLL) {
+        return SetError(SCA_E_SEQ_TOO_LONG, "flash: grid of " + std::to_string(blocks) +
+                                                " workgroups exceeds the launch limit");
+    }
+    if (const int rc =
+            EnsureLdsLimit<&flash_fwd_wide_kernel<E, D, kCausal>>(G::LDS_BYTES, "flash LDS limit")) {
+        return rc;
+    }
+    hipLaunchKernelGGL((flash_fwd_wide_kernel<E, D, kCausal>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(G::THREADS), G::LDS_BYTES, s, p, static_cast<int>(num_q_tiles));
+    return CheckLaunch("flash_fwd_wide_kernel", s);
 }
 
 template <typename E, int D, bool kCausal>
@@ -1645,14 +2476,14 @@ int LaunchForDim(const sca_flash_params& p, hipStream_t s) {
                 return LaunchFlashPair<E, 64>(p, s);
             }
             return DmaRowGroups(p, kCausal) == 2 ? LaunchFlashDma<E, 64, 2, kCausal>(p, s)
-                                                 : LaunchFlashDma<E, 64, 4, kCausal>(p, s);
+                                                 : LaunchFlashWide<E, 64, kCausal>(p, s);
         case 96: return LaunchFlash<E, 96, kCausal>(p, s);
         case 128:
             if (kCausal && UsePairKernel() && DmaRowGroups(p, kCausal) == 2) {
                 return LaunchFlashPair<E, 128>(p, s);
             }
             return DmaRowGroups(p, kCausal) == 2 ? LaunchFlashDma<E, 128, 2, kCausal>(p, s)
-                                                 : LaunchFlashDma<E, 128, 4, kCausal>(p, s);
+                                                 : LaunchFlashWide<E, 128, kCausal>(p, s);
         case 160: return LaunchFlash<E, 160, kCausal>(p, s);
         case 192: return LaunchFlash<E, 192, kCausal>(p, s);
         case 256: return LaunchFlash<E, 256, kCausal>(p, s);
@@ -1735,6 +2566,14 @@ int LdsBytesFor(int64_t head_dim) {
 using sca_hip::SetError;
 
 extern "C" {
+
+#if defined(SCA_MEASUREMENT_BUILD) && defined(SCA_STAMPS)
+// Measurement builds only: copies the wide kernel's region clocks ([blocks*4][9] uint32).
+int sca_hip_debug_wide_stamps(uint32_t* host, int64_t count) {
+    return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(sca_hip::g_wide_stamps),
+                                                static_cast<size_t>(count) * 4));
+}
+#endif
 
 int64_t sca_hip_flash_lds_bytes(int32_t head_dim, int64_t elem_bytes) {
     if (elem_bytes != 2) return -1;
