@@ -24,6 +24,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -355,7 +356,7 @@ def bench_copy(steps, warmup, mib=256):
 def cpu_baseline(max_seconds=12.0):
     import oracle.oracle as orc  # the CPU restatement is the timed baseline
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = host_threads()
     S, D = 4096, 128
     rng = np.random.default_rng(7)
     q = rng.standard_normal((1, 1, S, D), dtype=np.float32)
@@ -397,8 +398,50 @@ def cpu_baseline(max_seconds=12.0):
     return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"naive 3-pass FP32 restatement (attention_naive.cu:41-135) on one head of "
                       f"C2 (B=1,H=1,S=4096,D=128,causal), {runs} runs, {secs * 1e3:.1f} ms/run, "
-                      f"algorithmic causal FLOPs",
+                      f"algorithmic causal FLOPs, {threads} threads",
+            "host": host_cores(),
             "c1": c1}
+
+
+def host_cores():
+    """What the host reports: nproc (affinity-aware), std::thread::hardware_concurrency (the
+    online CPUs, as os.cpu_count), the affinity mask, and the CPU share one GPU job is given."""
+    try:
+        nproc = int(subprocess.run(["nproc"], capture_output=True, text=True, timeout=10).stdout)
+    except (OSError, ValueError, subprocess.SubprocessError):
+        nproc = None
+    share = os.environ.get("OMP_NUM_THREADS")
+    return {"nproc": nproc, "hardware_concurrency": os.cpu_count(),
+            "affinity": len(os.sched_getaffinity(0)),
+            "job_cpu_share": int(share) if share and share.isdigit() else None}
+
+
+def host_threads():
+    """All the cores this process may use: the affinity mask, capped by the per-job CPU share
+    the GPU box sets in OMP_NUM_THREADS (16 per GPU on this pool)."""
+    n = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS")
+    if share and share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return max(n, 1)
+
+
+def device_name(probe):
+    """The device's marketing name; HIP reports an empty name on some images, then rocm-smi's
+    product name (or the architecture) stands in."""
+    name = probe.name.decode().strip()
+    if name:
+        return name
+    try:
+        out = subprocess.run(["rocm-smi", "--showproductname", "--json"], capture_output=True,
+                             text=True, timeout=30).stdout
+        for card in json.loads(out).values():
+            for key in ("Card Series", "Card series", "Card Model", "Card model"):
+                if card.get(key):
+                    return str(card[key])
+    except (OSError, ValueError, subprocess.SubprocessError, AttributeError):
+        pass
+    return probe.arch_name.decode().split(":")[0]
 
 
 def load_traffic(name):
@@ -457,7 +500,7 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": "synthetic (seeded N(0,1))",
-        "device": {"name": probe.name.decode(), "arch": probe.arch_name.decode(),
+        "device": {"name": device_name(probe), "arch": probe.arch_name.decode(),
                    "cus": probe.cu_count},
     }
     if "c2_causal" in res:

@@ -285,3 +285,111 @@ def test_oracle_paged_kv_slots_are_page_times_block_plus_offset():
         lens[s] += n
         assert c.seq_len(s) == lens[s]
         assert c.block_count(s) == -(-lens[s] // 4)
+
+
+# ---- PagedKVCache restatement: properties the allocator's specification fixes -------------------
+# (paged_kv_cache.cpp:52-201 over block_manager.cpp:11-144: LIFO free list, all-or-nothing
+# allocation, table rows as long as the pool, revision bumped by every successful append or reset)
+
+def _pkv_snapshot(c, seqs):
+    return (c.page_table().copy(), [c.seq_len(s) for s in range(seqs)],
+            [c.block_count(s) for s in range(seqs)], c.stats())
+
+
+def test_oracle_paged_kv_failed_append_leaves_state_unchanged():
+    """An append the pool cannot serve changes nothing: table, lengths, counters, revision, and
+    the free list itself (the next allocation hands out the ids an untouched twin hands out)."""
+    bs = 4
+    a = orc.PagedKV(num_blocks=10, block_size=bs, max_num_seqs=3)
+    b = orc.PagedKV(num_blocks=10, block_size=bs, max_num_seqs=3)
+    for c in (a, b):
+        assert c.append(0, 13)[0] == 0      # 4 blocks
+        assert c.append(1, 9)[0] == 0       # 3 blocks
+        assert c.reset(0)[0] == 0           # 4 back on the stack
+        assert c.append(2, 5)[0] == 0       # 2 blocks: 5 used, 5 free
+    before = _pkv_snapshot(a, 3)
+    rc, slots, msg = a.append(0, 6 * bs)    # needs 6 blocks, 5 are free
+    assert rc == 2007 and slots == [] and "needs 6 more blocks but only 5 are free" in msg
+    rc, _, _ = a.append(1, 6 * bs)          # seq 1 holds 9 tokens in 3 blocks: needs 6 more
+    assert rc == 2007
+    after = _pkv_snapshot(a, 3)
+    assert np.array_equal(before[0], after[0]) and before[1:] == after[1:]
+    assert a.append(0, 5 * bs)[0] == 0 and b.append(0, 5 * bs)[0] == 0
+    assert np.array_equal(a.page_table(), b.page_table())
+    assert a.stats() == b.stats()
+
+
+def test_oracle_paged_kv_reset_returns_blocks_lifo_in_row_order():
+    """ResetSeq pushes the sequence's blocks back in row order, so the next allocation pops
+    them in reverse row order."""
+    c = orc.PagedKV(num_blocks=12, block_size=2, max_num_seqs=3)
+    # interleave two sequences so seq 0's row is not contiguous: 0,1 | 2 | 3,4 | 5 ...
+    assert c.append(0, 4)[0] == 0           # seq 0: blocks 0, 1
+    assert c.append(1, 2)[0] == 0           # seq 1: block 2
+    assert c.append(0, 3)[0] == 0           # seq 0: 7 tokens -> 4 blocks: + 3, 4
+    assert c.append(1, 1)[0] == 0           # seq 1: 3 tokens -> 2 blocks: + 5
+    row0 = c.page_table()[0, :4].tolist()
+    assert row0 == [0, 1, 3, 4]
+    assert c.reset(0)[0] == 0
+    assert c.page_table()[0].tolist() == [-1] * 12 and c.seq_len(0) == 0
+    # free stack (top last): 11 10 9 8 7 6 | 0 1 3 4  -> pops 4, 3, 1, 0, then 6, 7, ...
+    assert c.append(2, 2 * 6)[0] == 0
+    assert c.page_table()[2, :6].tolist() == [4, 3, 1, 0, 6, 7]
+
+
+def test_oracle_paged_kv_revision_counts_successful_appends_and_resets_only():
+    c = orc.PagedKV(num_blocks=4, block_size=4, max_num_seqs=2)
+    assert c.stats()["revision"] == 1 and c.stats()["synced_revision"] == 1
+    want = 1
+    ops = [("a", 0, 3, 0), ("a", 0, 1, 0), ("r", 1, 0, 0),         # reset of an empty seq counts
+           ("a", 1, 20, 2007), ("a", 2, 1, 2005), ("r", 5, 0, 2005),  # failures do not
+           ("a", 1, 8, 0), ("r", 0, 0, 0), ("a", 1, 9, 2007)]
+    for kind, seq, n, rc_want in ops:
+        rc = c.append(seq, n)[0] if kind == "a" else c.reset(seq)[0]
+        assert rc == rc_want, (kind, seq, n)
+        if rc == 0:
+            want += 1
+        assert c.stats()["revision"] == want, (kind, seq, n)
+    assert c.stats()["synced_revision"] == 1
+    c.sync()
+    assert c.stats()["synced_revision"] == want
+    st = c.stats()
+    assert (st["num_appends"], st["num_resets"]) == (3, 2)
+
+
+def test_oracle_paged_kv_block_conservation_over_a_random_trace():
+    """After every operation: used blocks = sum ceil(len/bs); every row lists exactly its
+    blocks, then -1; no block is owned twice; used + free = pool."""
+    nb, bs, seqs = 40, 4, 5
+    c = orc.PagedKV(num_blocks=nb, block_size=bs, max_num_seqs=seqs)
+    rng = np.random.default_rng(77)
+    for _ in range(400):
+        s = int(rng.integers(0, seqs))
+        if rng.random() < 0.15:
+            assert c.reset(s)[0] == 0
+        else:
+            c.append(s, int(rng.integers(1, 11)))
+        lens = [c.seq_len(i) for i in range(seqs)]
+        need = [-(-L // bs) for L in lens]
+        st = c.stats()
+        assert st["used_blocks"] == sum(need) and st["used_blocks"] + st["free_blocks"] == nb
+        pt = c.page_table()
+        owned = []
+        for i in range(seqs):
+            assert c.block_count(i) == need[i]
+            assert (pt[i, :need[i]] >= 0).all() and (pt[i, need[i]:] == -1).all()
+            owned += pt[i, :need[i]].tolist()
+        assert len(owned) == len(set(owned)) and all(0 <= b < nb for b in owned)
+
+
+def test_oracle_paged_kv_one_sequence_can_own_the_whole_pool():
+    """Rows are as long as the pool (paged_kv_cache.cpp:24-26), so a row never fills before the
+    pool does: the table-full rollback is unreachable and the first failure is capacity."""
+    nb, bs = 6, 3
+    c = orc.PagedKV(num_blocks=nb, block_size=bs, max_num_seqs=2)
+    assert c.append(0, nb * bs)[0] == 0
+    assert c.block_count(0) == nb and c.stats()["free_blocks"] == 0
+    assert sorted(c.page_table()[0].tolist()) == list(range(nb))
+    rc, _, msg = c.append(0, 1)
+    assert rc == 2007 and "needs 1 more blocks but only 0 are free" in msg
+    assert c.seq_len(0) == nb * bs
