@@ -272,50 +272,114 @@ def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=
 
 
 # ---- C5 through the host layer (PagedKVCache + sca::paged_attention) ------------------------------
-def bench_paged_host(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, lo=512, hi=16384):
-    """C5 as a serving loop drives it: the pool is filled through PagedKVCache::AppendTokens with
-    the page-sized appends of all sequences in a seeded random order (so every sequence's pages
-    are scattered over the pool), then each step appends one token to every sequence with one
-    AppendTokensBatch, syncs the page table (changed entries only) and calls
-    sca::paged_attention. The attend call is timed with HIP events around the API call
-    (dispatcher and allocation included); append + sync are timed the same way, separately."""
-    from sca_amd import host as SH
-    rng = np.random.default_rng(5006)
-    lengths = rng.integers(lo, hi + 1, size=num_seqs).astype(np.int64)
-    num_blocks = int(((lengths + steps + bs - 1) // bs).sum()) + 64
-    cache = SH.PagedKVCache(SH.KVCacheConfig(1, Hkv, D, bs, num_blocks, num_seqs, "bf16"))
-    chunk = SH.Tensor.from_numpy(bf16_bits(rng, (bs, Hkv, D)), "bf16")
-    order = np.concatenate([np.full((L + bs - 1) // bs, s) for s, L in enumerate(lengths)])
-    rng.shuffle(order)
-    filled = np.zeros(num_seqs, np.int64)
-    tails = {}
-    for s in order:
-        n = int(min(bs, lengths[s] - filled[s]))
-        if n == bs:
-            cache.append_tokens(int(s), 0, chunk, chunk)
-        else:
-            t = tails.setdefault(n, SH.Tensor.from_numpy(bf16_bits(rng, (n, Hkv, D)), "bf16"))
-            cache.append_tokens(int(s), 0, t, t)
-        filled[s] += n
-    q = SH.Tensor.from_numpy(bf16_bits(rng, (num_seqs, Hq, 1, D)), "bf16")
-    tok = SH.Tensor.from_numpy(bf16_bits(rng, (num_seqs, Hkv, D)), "bf16")
-    lens_dev = H.DeviceBuffer(num_seqs * 4)
-    ids = np.arange(num_seqs)
+class C5HostLoop:
+    """C5 as a serving loop drives it, through the public host API (include/sca_capi.h).
+
+    Fill: the page-sized appends of all sequences go through PagedKVCache::AppendTokens in a
+    seeded random order, so every sequence's pages are scattered over the pool; each append
+    takes its K and V rows from a bank of `bank` distinct seeded pages (a partial last page takes
+    the first rows of one). Step t: one AppendTokensBatch appends one token to every sequence
+    (token rows from a bank of 8 seeded [num_seqs, H_kv, D] tensors), SyncPageTable uploads the
+    changed entries, then sca::paged_attention attends with seq_lens including the new token.
+    `log` records every append (sequence, bank page or step token, rows) so a checker can rebuild
+    each sequence's K/V rows and the allocator trace."""
+
+    def __init__(self, steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, lo=512, hi=16384,
+                 seed=5006, bank=64):
+        from sca_amd import host as SH
+        self.SH = SH
+        self.num_seqs, self.bs, self.Hq, self.Hkv, self.D = num_seqs, bs, Hq, Hkv, D
+        rng = np.random.default_rng(seed)
+        self.lengths = rng.integers(lo, hi + 1, size=num_seqs).astype(np.int64)
+        self.num_blocks = int(((self.lengths + steps + bs - 1) // bs).sum()) + 64
+        self.cache = SH.PagedKVCache(SH.KVCacheConfig(1, Hkv, D, bs, self.num_blocks, num_seqs,
+                                                      "bf16"))
+        self.bank_k = bf16_bits(rng, (bank, bs, Hkv, D))
+        self.bank_v = bf16_bits(rng, (bank, bs, Hkv, D))
+        self.tok_k = bf16_bits(rng, (8, num_seqs, Hkv, D))
+        self.tok_v = bf16_bits(rng, (8, num_seqs, Hkv, D))
+        self.q_bits = bf16_bits(rng, (num_seqs, Hq, 1, D))
+        dev_k = [SH.Tensor.from_numpy(self.bank_k[i], "bf16") for i in range(bank)]
+        dev_v = [SH.Tensor.from_numpy(self.bank_v[i], "bf16") for i in range(bank)]
+        order = np.concatenate([np.full((L + bs - 1) // bs, s) for s, L in enumerate(self.lengths)])
+        rng.shuffle(order)
+        filled = np.zeros(num_seqs, np.int64)
+        self.log = []  # ("page", seq, bank index, rows) or ("token", seq, step)
+        tails = {}
+        for i, s in enumerate(order):
+            n = int(min(bs, self.lengths[s] - filled[s]))
+            j = (i * 7919) % bank
+            if n == bs:
+                self.cache.append_tokens(int(s), 0, dev_k[j], dev_v[j])
+            else:
+                key = (j, n)
+                if key not in tails:
+                    tails[key] = (SH.Tensor.from_numpy(np.ascontiguousarray(self.bank_k[j, :n]), "bf16"),
+                                  SH.Tensor.from_numpy(np.ascontiguousarray(self.bank_v[j, :n]), "bf16"))
+                self.cache.append_tokens(int(s), 0, *tails[key])
+            self.log.append(("page", int(s), j, n))
+            filled[s] += n
+        self.q = SH.Tensor.from_numpy(self.q_bits, "bf16")
+        self.toks = [(SH.Tensor.from_numpy(self.tok_k[i], "bf16"),
+                      SH.Tensor.from_numpy(self.tok_v[i], "bf16")) for i in range(8)]
+        self.lens_dev = H.DeviceBuffer(num_seqs * 4)
+        self.ids = np.arange(num_seqs)
+        self.cur = self.lengths.copy()
+        self.t = 0
+
+    def append_step(self):
+        """AppendTokensBatch (one token per sequence) and SyncPageTable."""
+        tk, tv = self.toks[self.t % 8]
+        self.cache.append_batch(self.ids, 0, tk, tv)
+        self.cache.sync_page_table()
+        for s in range(self.num_seqs):
+            self.log.append(("token", s, self.t))
+        self.cur = self.cur + 1
+        self.lens_dev.upload(self.cur.astype(np.int32))
+        self.t += 1
+
+    def attend(self):
+        """sca::paged_attention over every sequence (seq_lens include this step's token)."""
+        return self.SH.paged_attention(self.q, self.cache,
+                                       {"seq_lens": self.lens_dev.ptr, "num_seqs": self.num_seqs,
+                                        "block_size": self.bs})
+
+    def rows(self, seq):
+        """The K and V rows (bf16 bits, [L, H_kv, D]) sequence `seq` holds, in order."""
+        ks, vs = [], []
+        for e in self.log:
+            if e[1] != seq:
+                continue
+            if e[0] == "page":
+                ks.append(self.bank_k[e[2], :e[3]])
+                vs.append(self.bank_v[e[2], :e[3]])
+            else:
+                ks.append(self.tok_k[e[2] % 8, seq][None])
+                vs.append(self.tok_v[e[2] % 8, seq][None])
+        return np.concatenate(ks), np.concatenate(vs)
+
+    def step_bytes(self):
+        """Algorithmic bytes of the attend call: K+V once per KV head, page-table entries, Q+O."""
+        cur, bs = self.cur, self.bs
+        return int(cur.sum()) * self.Hkv * self.D * 2 * 2 + int(((cur + bs - 1) // bs).sum()) * 4 + \
+            2 * self.num_seqs * self.Hq * self.D * 2
+
+
+def bench_paged_host(steps):
+    """C5 through the public host API (C5HostLoop). The attend call is timed with HIP events
+    around the API call (dispatcher and allocation included); append + sync are timed the same
+    way, separately."""
+    loop = C5HostLoop(steps)
     start, mid, stop = H.Event(), H.Event(), H.Event()
-    cur = lengths.copy()
     t_attend = t_append = 0.0
     total_bytes = 0
     splits = None
     for step in range(steps + 2):  # two untimed warmup steps
         timed = step >= 2
         start.record()
-        cache.append_batch(ids, 0, tok, tok)
-        cache.sync_page_table()
-        cur = cur + 1
-        lens_dev.upload(cur.astype(np.int32))
+        loop.append_step()
         mid.record()
-        res = SH.paged_attention(q, cache, {"seq_lens": lens_dev.ptr, "num_seqs": num_seqs,
-                                            "block_size": bs})
+        res = loop.attend()
         stop.record()
         stop.synchronize()
         splits = res.stats.get("num_splits")
@@ -323,12 +387,11 @@ def bench_paged_host(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, lo=512, hi=
         if timed:
             t_append += start.elapsed_ms(mid)
             t_attend += mid.elapsed_ms(stop)
-            total_bytes += int(cur.sum()) * Hkv * D * 2 * 2 + \
-                int(((cur + bs - 1) // bs).sum()) * 4 + 2 * num_seqs * Hq * D * 2
+            total_bytes += loop.step_bytes()
     ms = t_attend / steps
     nbytes = total_bytes / steps
     return {"ms": ms, "gbps": nbytes / (ms * 1e-3) / 1e9, "append_sync_ms": t_append / steps,
-            "splits": splits, "num_blocks": num_blocks}
+            "splits": splits, "num_blocks": loop.num_blocks}
 
 
 # ---- copy calibration ------------------------------------------------------------------------------
@@ -436,9 +499,11 @@ def device_name(probe):
         out = subprocess.run(["rocm-smi", "--showproductname", "--json"], capture_output=True,
                              text=True, timeout=30).stdout
         for card in json.loads(out).values():
-            for key in ("Card Series", "Card series", "Card Model", "Card model"):
-                if card.get(key):
-                    return str(card[key])
+            for key in ("Card Series", "Card series", "Card Model", "Card model", "Card SKU",
+                        "Marketing Name", "Device Name"):
+                val = str(card.get(key, "")).strip()
+                if val and val.upper() != "N/A":
+                    return val
     except (OSError, ValueError, subprocess.SubprocessError, AttributeError):
         pass
     return probe.arch_name.decode().split(":")[0]
