@@ -163,6 +163,14 @@ SCA_CAPI int sca_pkv_append(ScaPagedKV* c, int64_t seq_id, int64_t layer, const 
 SCA_CAPI int sca_pkv_append_batch(ScaPagedKV* c, const int64_t* seq_ids, int64_t num_entries,
                                   int64_t layer, const ScaTensor* k_new, const ScaTensor* v_new,
                                   void* stream);
+/* Multi-layer appends (sca::PagedKVCache::ReserveTokens / ReserveTokensBatch /
+ * WriteReservedLayer; no reference counterpart): reserve pages and slots and advance the lengths
+ * once, then write each layer's K/V rows into the reserved slots. */
+SCA_CAPI int sca_pkv_reserve(ScaPagedKV* c, int64_t seq_id, int64_t num_tokens, void* stream);
+SCA_CAPI int sca_pkv_reserve_batch(ScaPagedKV* c, const int64_t* seq_ids, int64_t num_entries,
+                                   void* stream);
+SCA_CAPI int sca_pkv_write_layer(ScaPagedKV* c, int64_t layer, const ScaTensor* k_new,
+                                 const ScaTensor* v_new, void* stream);
 SCA_CAPI int sca_pkv_reset(ScaPagedKV* c, int64_t seq_id, void* stream);
 SCA_CAPI int sca_pkv_sync(ScaPagedKV* c, void* stream);
 SCA_CAPI int sca_pkv_force_sync(ScaPagedKV* c, void* stream);

@@ -28,7 +28,8 @@ namespace sca {
 //   * slot mappings (and the page ids ResetSeq clears) are staged in pinned host memory and copied
 //     on the caller's stream.
 // As in the reference, AppendTokens advances the sequence length on every call whatever the
-// layer, so one call per token (layer 0) is the supported usage.
+// layer, so one call per token (layer 0) is its supported usage; multi-layer callers reserve the
+// tokens once and write each layer (ReserveTokens / WriteReservedLayer).
 class SCI_ATTENTION_API PagedKVCache {
 public:
     PagedKVCache() = default;
@@ -57,6 +58,22 @@ public:
                                   const sci::Tensor& k_new, const sci::Tensor& v_new,
                                   sci::Stream* stream);
 
+    // Multi-layer appends (no counterpart in the reference, whose AppendTokens advances the
+    // length on every call whatever the layer, so a model with several layers cannot store one
+    // token per layer through it). A reservation allocates the pages, extends the rows, uploads
+    // the slots and advances the lengths once: the host state afterwards (pages, their order,
+    // rows, lengths, revision, append count) equals that of AppendTokens / AppendTokensBatch for
+    // the same tokens, but no K/V is written. WriteReservedLayer then scatters one layer's K/V
+    // rows ([reserved, num_kv_heads, head_dim], in reservation order) into the reserved slots;
+    // a model calls it once per layer as its layers produce K and V. The reservation holds until
+    // the next Reserve*, AppendTokens*, or ResetSeq call (they reuse the slot buffer).
+    sci::Status ReserveTokens(int64_t seq_id, int64_t num_tokens, sci::Stream* stream);
+    sci::Status ReserveTokensBatch(const int64_t* seq_ids, int64_t num_entries,
+                                   sci::Stream* stream);
+    sci::Status WriteReservedLayer(int64_t layer, const sci::Tensor& k_new,
+                                   const sci::Tensor& v_new, sci::Stream* stream);
+    int64_t ReservedTokens() const noexcept { return reserved_tokens_; }
+
     // Zeroes the sequence's pages, returns them to the pool and clears its row.
     sci::Status ResetSeq(int64_t seq_id, sci::Stream* stream);
 
@@ -82,6 +99,11 @@ public:
     uint64_t SyncedRevision() const noexcept { return synced_revision_; }
 
 private:
+    sci::Status ReserveSlots(int64_t seq_id, int64_t num_new, const char* who, sci::Stream* stream);
+    sci::Status ReserveBatchSlots(const int64_t* seq_ids, int64_t num_entries, const char* who,
+                                  sci::Stream* stream);
+    sci::Status CheckTokenRows(const sci::Tensor& k_new, const sci::Tensor& v_new, int64_t rows,
+                               const char* who) const;
     sci::Result<int32_t*> Staging(int64_t entries);
     sci::Status StagingSubmitted(void* stream, bool blocking);
     void ReleaseStaging() noexcept;
@@ -97,6 +119,7 @@ private:
     sci::Tensor page_table_device_;
     sci::Tensor slot_mapping_device_;       // slots of the last append / ids of the last reset
     int64_t slot_mapping_capacity_{0};
+    int64_t reserved_tokens_{0};            // slots of the last reservation (0: none)
     sci::Tensor pairs_device_;              // (index, value) pairs of the last sparse sync
     int64_t pairs_capacity_{0};
     int32_t* staging_host_{nullptr};        // pinned host staging for both uploads

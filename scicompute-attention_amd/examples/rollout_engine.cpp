@@ -1,20 +1,28 @@
 // Rollout-style serving loop over the public sca:: API at the Qwen3-4B attention shape
-// (H_q = 32, H_kv = 8, D = 128, fp16, 16-token pages): the role of the reference's
-// examples/rollout_engine_stub.cpp:138-334, arranged for this build.
+// (36 layers, H_q = 32, H_kv = 8, D = 128, fp16, 16-token pages): the role of the reference's
+// examples/rollout_engine_stub.cpp:138-334, arranged for this build. Every step drives all the
+// layers, as a model does:
 //
-//   prefill  every prompt of the batch in ONE flash_attention_varlen call over packed
-//            [tokens, heads, dim] buffers (causal), then one AppendTokens per request;
-//   decode   per step: one AppendTokensBatch (a token for every request), SyncPageTable
-//            (changed entries only), the lengths uploaded AFTER they advanced (the reference
-//            uploads them before the increment, examples/rollout_engine_stub.cpp:253-254 vs
-//            280, so its attention misses the token just appended), then one paged_attention.
+//   prefill  one ReserveTokensBatch for every prompt token of the batch (the packed token order),
+//            then per layer: one causal flash_attention_varlen over that layer's packed
+//            [tokens, heads, dim] Q/K/V and one WriteReservedLayer of its K/V;
+//   decode   per step: one ReserveTokensBatch (a token for every request: pages, slots and
+//            lengths advance once), SyncPageTable (changed entries only), the lengths uploaded
+//            AFTER they advanced (the reference uploads them before the increment,
+//            examples/rollout_engine_stub.cpp:253-254 vs 280, so its attention misses the token
+//            just appended), then per layer: WriteReservedLayer + paged_attention(layer).
 //
-// One attention layer is driven, as in the reference (layer 0, rollout_engine_stub.cpp:226,
-// 246): AppendTokens advances a sequence's length on every call, so multi-layer writes are not
-// expressible through that interface. Timings are GPU time from HIP events around each API
-// call (dispatch and allocation included). Prints a summary; --json PATH writes it as JSON.
+// The reference drives layer 0 only (rollout_engine_stub.cpp:226, 246): its AppendTokens advances
+// a sequence's length on every call, so it cannot store one token in several layers.
+// Synthetic activations: each layer reads its Q/K/V as a window of a seeded bank shifted by a
+// per-layer (and, in decode, per-step) row offset, so every layer sees different data.
+// Timings are GPU time from HIP events (dispatch and allocation included). Prints a summary;
+// --json PATH writes it as JSON; --dump DIR writes sampled (layer, sequence) inputs and outputs
+// of the prefill and of the first and last decode step as raw fp16 files plus manifest.json,
+// for an external check against an attention oracle.
 //
-//   rollout_engine [--requests N] [--max-new T] [--min-prompt P] [--json PATH]
+//   rollout_engine [--requests N] [--max-new T] [--min-prompt P] [--layers L] [--json PATH]
+//                  [--dump DIR]
 
 #include <algorithm>
 #include <cstdio>
@@ -34,12 +42,18 @@ constexpr int64_t kHeadsQ = 32;
 constexpr int64_t kHeadsKv = 8;
 constexpr int64_t kHeadDim = 128;
 constexpr int64_t kBlockSize = 16;
+constexpr int64_t kLayerShift = 7;        // prefill bank rows between consecutive layers
+constexpr int64_t kDecodeWindow = 2048;   // decode bank rows beyond the batch
+
+int64_t DecodeShift(int64_t layer, int64_t step) { return (layer * 37 + step * 11) % kDecodeWindow; }
 
 struct Args {
     int64_t requests = 16;
     int64_t max_new = 32;
     int64_t min_prompt = 256;
+    int64_t layers = 36;
     std::string json;
+    std::string dump;
 };
 
 Args Parse(int argc, char** argv) {
@@ -49,7 +63,9 @@ Args Parse(int argc, char** argv) {
         if (k == "--requests") a.requests = std::atoll(argv[i + 1]);
         else if (k == "--max-new") a.max_new = std::atoll(argv[i + 1]);
         else if (k == "--min-prompt") a.min_prompt = std::atoll(argv[i + 1]);
+        else if (k == "--layers") a.layers = std::atoll(argv[i + 1]);
         else if (k == "--json") a.json = argv[i + 1];
+        else if (k == "--dump") a.dump = argv[i + 1];
     }
     return a;
 }
@@ -69,10 +85,8 @@ uint16_t HalfBits(float f) {
     return static_cast<uint16_t>(h);
 }
 
-// Seeded fp16 bits in [-scale, scale] (xorshift32), uploaded to a new device tensor.
-sci::Tensor RandomHalf(const std::vector<int64_t>& dims, uint32_t seed, float scale) {
-    int64_t n = 1;
-    for (int64_t d : dims) n *= d;
+// Seeded fp16 bits in [-scale, scale] (xorshift32).
+std::vector<uint16_t> RandomBits(int64_t n, uint32_t seed, float scale) {
     std::vector<uint16_t> bits(static_cast<size_t>(n));
     uint32_t s = seed ? seed : 1u;
     for (auto& b : bits) {
@@ -81,10 +95,7 @@ sci::Tensor RandomHalf(const std::vector<int64_t>& dims, uint32_t seed, float sc
         s ^= s << 5;
         b = HalfBits(scale * (-1.0f + 2.0f * static_cast<float>(s) / 4294967295.0f));
     }
-    sci::Device& dev = sci::GpuDevice(0);
-    sci::Tensor t(sci::TensorShape(dims), sci::DType::kFloat16, dev);
-    if (t.data() != nullptr) dev.copy_to_device(t.data(), bits.data(), bits.size() * 2);
-    return t;
+    return bits;
 }
 
 struct Timer {
@@ -122,6 +133,58 @@ int Fail(const char* what, const sci::Status& st) {
     return 4;
 }
 
+// A seeded fp16 bank: host bits (kept for the dump) and the device copy.
+struct Bank {
+    std::vector<uint16_t> host;
+    sci::Tensor dev;
+    int64_t row_elems = 0;  // elements per token row
+};
+
+Bank MakeBank(int64_t rows, int64_t heads, uint32_t seed, float scale) {
+    Bank b;
+    b.row_elems = heads * kHeadDim;
+    b.host = RandomBits(rows * b.row_elems, seed, scale);
+    sci::Device& dev = sci::GpuDevice(0);
+    b.dev = sci::Tensor(sci::TensorShape({rows, heads, kHeadDim}), sci::DType::kFloat16, dev);
+    if (b.dev.data() != nullptr) dev.copy_to_device(b.dev.data(), b.host.data(), b.host.size() * 2);
+    return b;
+}
+
+// A device view of `rows` token rows starting at row `first`, shaped `dims`.
+sci::Tensor View(Bank& b, int64_t first, std::vector<int64_t> dims) {
+    return sci::Tensor(sci::TensorShape(std::move(dims)), sci::DType::kFloat16,
+                       sci::GpuDevice(0),
+                       static_cast<uint16_t*>(b.dev.data()) + first * b.row_elems);
+}
+
+// Appends rows [first, first + n) of a bank (host bits) to dst.
+void AppendRows(std::vector<uint16_t>& dst, const Bank& b, int64_t first, int64_t n) {
+    const auto* p = b.host.data() + first * b.row_elems;
+    dst.insert(dst.end(), p, p + n * b.row_elems);
+}
+
+struct Dumper {
+    std::string dir;
+    std::string manifest;
+    int count = 0;
+    bool on() const { return !dir.empty(); }
+    void Write(const std::string& tag, const void* data, size_t bytes,
+               const std::vector<int64_t>& shape) {
+        const std::string file = tag + ".f16";
+        std::ofstream f(dir + "/" + file, std::ios::binary);
+        f.write(static_cast<const char*>(data), static_cast<std::streamsize>(bytes));
+        manifest += std::string(count++ ? ",\n" : "") + "  \"" + tag + "\": [";
+        for (size_t i = 0; i < shape.size(); ++i) {
+            manifest += (i ? ", " : "") + std::to_string(shape[i]);
+        }
+        manifest += "]";
+    }
+    void Finish(const std::string& extra) {
+        std::ofstream f(dir + "/manifest.json");
+        f << "{\"arrays\": {\n" << manifest << "\n}, " << extra << "}\n";
+    }
+};
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -133,6 +196,11 @@ int main(int argc, char** argv) {
     }
     sci::Device& device = sci::GpuDevice(0);
     const int64_t n = args.requests;
+    const int64_t layers = args.layers;
+    if (n < 1 || layers < 1 || args.max_new < 1) {
+        std::printf("[rollout] --requests, --layers and --max-new must be positive\n");
+        return 1;
+    }
 
     // Uneven prompt lengths, like a real rollout batch.
     std::vector<int32_t> prompt(static_cast<size_t>(n));
@@ -145,7 +213,7 @@ int main(int argc, char** argv) {
     const int64_t max_prompt = *std::max_element(prompt.begin(), prompt.end());
 
     sca::KVCacheConfig kv;
-    kv.num_layers = 1;
+    kv.num_layers = layers;
     kv.num_kv_heads = kHeadsKv;
     kv.head_dim = kHeadDim;
     kv.block_size = kBlockSize;
@@ -163,53 +231,87 @@ int main(int argc, char** argv) {
     if (!created.ok()) return Fail("PagedKVCache::Create", created.error());
     sca::PagedKVCache cache = std::move(*created);
 
-    // ---- prefill: the whole batch in one packed launch ------------------------------------------
-    sci::Tensor q = RandomHalf({total, kHeadsQ, kHeadDim}, 1000, 1.0f);
-    sci::Tensor k = RandomHalf({total, kHeadsKv, kHeadDim}, 2000, 1.0f);
-    sci::Tensor v = RandomHalf({total, kHeadsKv, kHeadDim}, 3000, 0.5f);
+    Dumper dump{args.dump};
+    // Sampled (layer, sequence) pairs for the dump.
+    const std::vector<int64_t> dump_layers = {0, layers / 2, layers - 1};
+    const std::vector<int64_t> dump_seqs = {0, std::min<int64_t>(1, n - 1)};
+    auto dumped_layer = [&](int64_t l) {
+        return dump.on() && std::find(dump_layers.begin(), dump_layers.end(), l) != dump_layers.end();
+    };
+
+    // ---- prefill: reserve every prompt token once, then each layer --------------------------------
+    // Layer l reads bank rows [l * kLayerShift, l * kLayerShift + total).
+    Bank pq = MakeBank(total + layers * kLayerShift, kHeadsQ, 1000, 1.0f);
+    Bank pk = MakeBank(total + layers * kLayerShift, kHeadsKv, 2000, 1.0f);
+    Bank pv = MakeBank(total + layers * kLayerShift, kHeadsKv, 3000, 0.5f);
+    std::vector<int64_t> packed_ids;
+    packed_ids.reserve(static_cast<size_t>(total));
+    for (int64_t r = 0; r < n; ++r) packed_ids.insert(packed_ids.end(), prompt[static_cast<size_t>(r)], r);
     sca::AttentionConfig pcfg;
     pcfg.backend = sca::BackendKind::kFlash;
     pcfg.causal = true;
     Timer timer;
     // One untimed call first: code-object loading and first-use allocations are not serving time.
-    if (!sca::flash_attention_varlen(q, k, v, n, cu.data(), cu.data(), max_prompt, max_prompt,
-                                     pcfg).ok()) {
+    if (!sca::flash_attention_varlen(View(pq, 0, {total, kHeadsQ, kHeadDim}),
+                                     View(pk, 0, {total, kHeadsKv, kHeadDim}),
+                                     View(pv, 0, {total, kHeadsKv, kHeadDim}), n, cu.data(),
+                                     cu.data(), max_prompt, max_prompt, pcfg).ok()) {
         std::printf("[rollout] warm-up prefill failed\n");
         return 4;
     }
+    double prefill_attend_ms = 0.0;
     timer.Start();
-    const auto pre = sca::flash_attention_varlen(q, k, v, n, cu.data(), cu.data(), max_prompt,
-                                                 max_prompt, pcfg);
-    const double prefill_ms = timer.StopMs();
-    if (!pre.ok()) return Fail("prefill", pre.error());
+    sci::Status st = cache.ReserveTokensBatch(packed_ids.data(), total, nullptr);
+    if (!st.ok()) return Fail("prompt reservation", st);
+    const double prompt_reserve_ms = timer.StopMs();
+    double prompt_write_ms = 0.0;
+    for (int64_t l = 0; l < layers; ++l) {
+        const int64_t off = l * kLayerShift;
+        const sci::Tensor kl = View(pk, off, {total, kHeadsKv, kHeadDim});
+        const sci::Tensor vl = View(pv, off, {total, kHeadsKv, kHeadDim});
+        timer.Start();
+        const auto pre = sca::flash_attention_varlen(View(pq, off, {total, kHeadsQ, kHeadDim}), kl,
+                                                     vl, n, cu.data(), cu.data(), max_prompt,
+                                                     max_prompt, pcfg);
+        prefill_attend_ms += timer.StopMs();
+        if (!pre.ok()) return Fail("prefill", pre.error());
+        timer.Start();
+        st = cache.WriteReservedLayer(l, kl, vl, nullptr);
+        prompt_write_ms += timer.StopMs();
+        if (!st.ok()) return Fail("prompt layer write", st);
+        if (dumped_layer(l)) {
+            std::vector<uint16_t> out(static_cast<size_t>(total * kHeadsQ * kHeadDim));
+            device.copy_to_host(out.data(), pre->out.data(), out.size() * 2);
+            for (int64_t r : dump_seqs) {
+                const int64_t a = cu[static_cast<size_t>(r)], L = prompt[static_cast<size_t>(r)];
+                const std::string tag = "prefill_l" + std::to_string(l) + "_s" + std::to_string(r);
+                std::vector<uint16_t> q, k, v;
+                AppendRows(q, pq, off + a, L);
+                AppendRows(k, pk, off + a, L);
+                AppendRows(v, pv, off + a, L);
+                dump.Write(tag + "_q", q.data(), q.size() * 2, {L, kHeadsQ, kHeadDim});
+                dump.Write(tag + "_k", k.data(), k.size() * 2, {L, kHeadsKv, kHeadDim});
+                dump.Write(tag + "_v", v.data(), v.size() * 2, {L, kHeadsKv, kHeadDim});
+                dump.Write(tag + "_out", out.data() + a * kHeadsQ * kHeadDim,
+                           static_cast<size_t>(L * kHeadsQ * kHeadDim) * 2, {L, kHeadsQ, kHeadDim});
+            }
+        }
+    }
     double prefill_flops = 0.0;
     for (int32_t L : prompt) prefill_flops += 4.0 * kHeadsQ * kHeadDim * (0.5 * L * (L + 1.0));
-
-    timer.Start();
-    const int64_t kv_token_bytes = kHeadsKv * kHeadDim * 2;
-    for (int64_t r = 0; r < n; ++r) {
-        const int64_t off = cu[static_cast<size_t>(r)] * kv_token_bytes;
-        const int64_t len = prompt[static_cast<size_t>(r)];
-        sci::Tensor kr(sci::TensorShape({len, kHeadsKv, kHeadDim}), sci::DType::kFloat16, device,
-                       static_cast<char*>(k.data()) + off);
-        sci::Tensor vr(sci::TensorShape({len, kHeadsKv, kHeadDim}), sci::DType::kFloat16, device,
-                       static_cast<char*>(v.data()) + off);
-        const sci::Status st = cache.AppendTokens(r, 0, kr, vr, nullptr);
-        if (!st.ok()) return Fail("prompt append", st);
-    }
-    const double prompt_append_ms = timer.StopMs();
+    prefill_flops *= static_cast<double>(layers);
 
     // ---- decode loop ----------------------------------------------------------------------------
+    // Step s, layer l reads bank rows [DecodeShift(l, s), DecodeShift(l, s) + n).
+    Bank dq = MakeBank(n + kDecodeWindow, kHeadsQ, 5000, 1.0f);
+    Bank dk = MakeBank(n + kDecodeWindow, kHeadsKv, 6000, 1.0f);
+    Bank dv = MakeBank(n + kDecodeWindow, kHeadsKv, 7000, 0.5f);
     std::vector<int64_t> ids(static_cast<size_t>(n));
     for (int64_t r = 0; r < n; ++r) ids[static_cast<size_t>(r)] = r;
     std::vector<int32_t> lens(prompt);
     sci::Tensor seq_lens(sci::TensorShape({n}), sci::DType::kInt32, device);
-    sci::Tensor q_step = RandomHalf({n, kHeadsQ, 1, kHeadDim}, 5000, 1.0f);
-    sci::Tensor k_step = RandomHalf({n, kHeadsKv, kHeadDim}, 6000, 1.0f);
-    sci::Tensor v_step = RandomHalf({n, kHeadsKv, kHeadDim}, 7000, 0.5f);
     sca::AttentionConfig dcfg;
     dcfg.backend = sca::BackendKind::kPaged;
-    std::vector<double> append_ms, attend_ms;
     {
         // Untimed attend over the prompts (kernel loading, scratch allocation).
         device.copy_to_device(seq_lens.data(), lens.data(), lens.size() * sizeof(int32_t));
@@ -217,66 +319,140 @@ int main(int argc, char** argv) {
         params.seq_lens = static_cast<const int32_t*>(seq_lens.data());
         params.num_seqs = n;
         params.block_size = kBlockSize;
-        const sci::Status st = cache.SyncPageTable(nullptr);
-        if (!st.ok() || !sca::paged_attention(q_step, cache, params, dcfg).ok()) {
+        st = cache.SyncPageTable(nullptr);
+        if (!st.ok() || !sca::paged_attention(View(dq, 0, {n, kHeadsQ, 1, kHeadDim}), cache, params,
+                                              dcfg).ok()) {
             std::printf("[rollout] warm-up decode failed\n");
             return 4;
         }
     }
+    std::vector<void*> ev(static_cast<size_t>(2 * layers + 2));
+    for (auto& e : ev) sca_hip_event_create(&e);
+    std::vector<double> step_ms, attend_ms, append_ms;
     double attend_bytes = 0.0;
     for (int64_t step = 0; step < args.max_new; ++step) {
-        timer.Start();
-        sci::Status st = cache.AppendTokensBatch(ids.data(), n, 0, k_step, v_step, nullptr);
-        if (!st.ok()) return Fail("decode append", st);
+        const bool dump_step = dump.on() && (step == 0 || step == args.max_new - 1);
+        sca_hip_event_record(ev[0], nullptr);
+        st = cache.ReserveTokensBatch(ids.data(), n, nullptr);
+        if (!st.ok()) return Fail("decode reservation", st);
         st = cache.SyncPageTable(nullptr);
         if (!st.ok()) return Fail("page-table sync", st);
         for (auto& L : lens) ++L;  // the new token is attended in this step
         device.copy_to_device(seq_lens.data(), lens.data(), lens.size() * sizeof(int32_t));
-        append_ms.push_back(timer.StopMs());
-
         sca::PagedAttentionParams params;
         params.page_table = cache.PageTableDevicePtr();
         params.seq_lens = static_cast<const int32_t*>(seq_lens.data());
         params.num_seqs = n;
         params.block_size = kBlockSize;
         params.max_blocks_per_seq = cache.MaxBlocksPerSeq();
-        params.layer = 0;
-        timer.Start();
-        const auto out = sca::paged_attention(q_step, cache, params, dcfg);
-        attend_ms.push_back(timer.StopMs());
-        if (!out.ok()) return Fail("paged attention", out.error());
-        for (int32_t L : lens) attend_bytes += 2.0 * L * kv_token_bytes;
+        for (int64_t l = 0; l < layers; ++l) {
+            const int64_t off = DecodeShift(l, step);
+            st = cache.WriteReservedLayer(l, View(dk, off, {n, kHeadsKv, kHeadDim}),
+                                          View(dv, off, {n, kHeadsKv, kHeadDim}), nullptr);
+            if (!st.ok()) return Fail("decode layer write", st);
+            params.layer = l;
+            sca_hip_event_record(ev[static_cast<size_t>(1 + 2 * l)], nullptr);
+            const auto out = sca::paged_attention(View(dq, off, {n, kHeadsQ, 1, kHeadDim}), cache,
+                                                  params, dcfg);
+            sca_hip_event_record(ev[static_cast<size_t>(2 + 2 * l)], nullptr);
+            if (!out.ok()) return Fail("paged attention", out.error());
+            if (dump_step && dumped_layer(l)) {
+                std::vector<uint16_t> o(static_cast<size_t>(n * kHeadsQ * kHeadDim));
+                device.copy_to_host(o.data(), out->out.data(), o.size() * 2);
+                for (int64_t r : dump_seqs) {
+                    const std::string tag = "decode" + std::to_string(step) + "_l" +
+                                            std::to_string(l) + "_s" + std::to_string(r);
+                    std::vector<uint16_t> q, k, v;
+                    AppendRows(q, dq, off + r, 1);
+                    // History: the prompt rows of this layer, then this layer's decode rows.
+                    AppendRows(k, pk, l * kLayerShift + cu[static_cast<size_t>(r)],
+                               prompt[static_cast<size_t>(r)]);
+                    AppendRows(v, pv, l * kLayerShift + cu[static_cast<size_t>(r)],
+                               prompt[static_cast<size_t>(r)]);
+                    for (int64_t s2 = 0; s2 <= step; ++s2) {
+                        AppendRows(k, dk, DecodeShift(l, s2) + r, 1);
+                        AppendRows(v, dv, DecodeShift(l, s2) + r, 1);
+                    }
+                    const int64_t L = lens[static_cast<size_t>(r)];
+                    dump.Write(tag + "_q", q.data(), q.size() * 2, {1, kHeadsQ, kHeadDim});
+                    dump.Write(tag + "_k", k.data(), k.size() * 2, {L, kHeadsKv, kHeadDim});
+                    dump.Write(tag + "_v", v.data(), v.size() * 2, {L, kHeadsKv, kHeadDim});
+                    dump.Write(tag + "_out", o.data() + r * kHeadsQ * kHeadDim,
+                               static_cast<size_t>(kHeadsQ * kHeadDim) * 2, {1, kHeadsQ, kHeadDim});
+                }
+            }
+        }
+        sca_hip_event_record(ev.back(), nullptr);
+        sca_hip_event_synchronize(ev.back());
+        float ms = 0.0f;
+        sca_hip_event_elapsed_ms(&ms, ev[0], ev.back());
+        if (!dump_step) step_ms.push_back(ms);
+        double attend = 0.0;
+        for (int64_t l = 0; l < layers; ++l) {
+            sca_hip_event_elapsed_ms(&ms, ev[static_cast<size_t>(1 + 2 * l)],
+                                     ev[static_cast<size_t>(2 + 2 * l)]);
+            attend += ms;
+        }
+        if (!dump_step) {
+            attend_ms.push_back(attend);
+            append_ms.push_back(step_ms.back() - attend);
+            for (int32_t L : lens) attend_bytes += 2.0 * L * kHeadsKv * kHeadDim * 2 * layers;
+        }
+    }
+    for (auto& e : ev) sca_hip_event_destroy(e);
+    if (step_ms.empty()) {  // every step was a dump step
+        step_ms.push_back(0.0);
+        attend_ms.push_back(0.0);
+        append_ms.push_back(0.0);
     }
 
-    double attend_total = 0.0, append_total = 0.0;
+    double attend_total = 0.0, step_total = 0.0;
     for (double t : attend_ms) attend_total += t;
-    for (double t : append_ms) append_total += t;
+    for (double t : step_ms) step_total += t;
     const int64_t generated = n * args.max_new;
-    const double step_ms = (attend_total + append_total) / static_cast<double>(args.max_new);
+    const double mean_step = step_total / static_cast<double>(step_ms.size());
+    const double tokens_per_s = mean_step > 0.0 ? static_cast<double>(n) / (mean_step * 1e-3) : 0.0;
+    const double attend_gbps = attend_total > 0.0 ? attend_bytes / (attend_total * 1e-3) / 1e9 : 0.0;
+    const double prefill_tflops = prefill_flops / (prefill_attend_ms * 1e-3) / 1e12;
     const auto stats = cache.Stats();
-    std::printf("[rollout] requests=%lld prompts=[%d..%d] tokens=%lld max_new=%lld\n",
-                static_cast<long long>(n), *std::min_element(prompt.begin(), prompt.end()),
-                static_cast<int>(max_prompt), static_cast<long long>(total),
-                static_cast<long long>(args.max_new));
-    std::printf("[rollout] prefill  %.3f ms (one varlen launch, %.1f TFLOP/s); prompt appends %.3f ms\n",
-                prefill_ms, prefill_flops / (prefill_ms * 1e-3) / 1e12, prompt_append_ms);
-    std::printf("[rollout] decode   attend P50=%.3f ms P99=%.3f ms (%.0f GB/s); append+sync P50=%.3f ms\n",
-                Percentile(attend_ms, 0.5), Percentile(attend_ms, 0.99),
-                attend_bytes / (attend_total * 1e-3) / 1e9, Percentile(append_ms, 0.5));
-    std::printf("[rollout] tokens/s per layer=%.0f used_blocks=%lld/%lld\n",
-                static_cast<double>(n) / (step_ms * 1e-3), static_cast<long long>(stats.used_blocks),
+    std::printf("[rollout] requests=%lld layers=%lld prompts=[%d..%d] tokens=%lld max_new=%lld\n",
+                static_cast<long long>(n), static_cast<long long>(layers),
+                *std::min_element(prompt.begin(), prompt.end()), static_cast<int>(max_prompt),
+                static_cast<long long>(total), static_cast<long long>(args.max_new));
+    std::printf("[rollout] prefill  attention %.3f ms over %lld layers (%.1f TFLOP/s); reserve %.3f ms, "
+                "layer writes %.3f ms\n",
+                prefill_attend_ms, static_cast<long long>(layers), prefill_tflops, prompt_reserve_ms,
+                prompt_write_ms);
+    std::printf("[rollout] decode   step P50=%.3f ms P99=%.3f ms (all layers); attention %.3f ms/step "
+                "(%.0f GB/s); reserve+sync+writes %.3f ms/step\n",
+                Percentile(step_ms, 0.5), Percentile(step_ms, 0.99), Percentile(attend_ms, 0.5),
+                attend_gbps, Percentile(append_ms, 0.5));
+    std::printf("[rollout] decode tokens/s=%.0f (attention and cache only) used_blocks=%lld/%lld\n",
+                tokens_per_s, static_cast<long long>(stats.used_blocks),
                 static_cast<long long>(stats.num_blocks));
+    if (dump.on()) {
+        std::string seqs = "[";
+        for (size_t i = 0; i < dump_seqs.size(); ++i) seqs += (i ? ", " : "") + std::to_string(dump_seqs[i]);
+        std::string lay = "[";
+        for (size_t i = 0; i < dump_layers.size(); ++i) lay += (i ? ", " : "") + std::to_string(dump_layers[i]);
+        dump.Finish("\"layers\": " + lay + "], \"seqs\": " + seqs + "], \"max_new\": " +
+                    std::to_string(args.max_new));
+    }
     if (!args.json.empty()) {
         std::ofstream f(args.json);
-        f << "{\"engine\": \"rollout_engine\", \"requests\": " << n << ", \"max_new_tokens\": "
-          << args.max_new << ", \"prompt_tokens\": " << total << ", \"prefill_ms\": " << prefill_ms
-          << ", \"prefill_tflops\": " << prefill_flops / (prefill_ms * 1e-3) / 1e12
-          << ", \"decode_attend_ms\": {\"p50\": " << Percentile(attend_ms, 0.5) << ", \"p99\": "
-          << Percentile(attend_ms, 0.99) << "}, \"decode_append_sync_ms_p50\": "
-          << Percentile(append_ms, 0.5) << ", \"decode_attend_gbps\": "
-          << attend_bytes / (attend_total * 1e-3) / 1e9 << ", \"generated_tokens\": " << generated
-          << ", \"kv_blocks_used\": " << stats.used_blocks << ", \"shape\": {\"Hq\": " << kHeadsQ
-          << ", \"Hkv\": " << kHeadsKv << ", \"D\": " << kHeadDim << "}}\n";
+        f << "{\"engine\": \"rollout_engine\", \"requests\": " << n << ", \"layers\": " << layers
+          << ", \"max_new_tokens\": " << args.max_new << ", \"prompt_tokens\": " << total
+          << ", \"prefill_attention_ms\": " << prefill_attend_ms << ", \"prefill_tflops\": "
+          << prefill_tflops << ", \"prompt_reserve_ms\": " << prompt_reserve_ms
+          << ", \"prompt_layer_writes_ms\": " << prompt_write_ms
+          << ", \"decode_step_ms\": {\"p50\": " << Percentile(step_ms, 0.5) << ", \"p99\": "
+          << Percentile(step_ms, 0.99) << "}, \"decode_attention_ms_p50\": "
+          << Percentile(attend_ms, 0.5) << ", \"decode_reserve_sync_writes_ms_p50\": "
+          << Percentile(append_ms, 0.5) << ", \"decode_attend_gbps\": " << attend_gbps
+          << ", \"decode_tokens_per_s\": " << tokens_per_s << ", \"generated_tokens\": "
+          << generated << ", \"kv_blocks_used\": " << stats.used_blocks
+          << ", \"shape\": {\"Hq\": " << kHeadsQ << ", \"Hkv\": " << kHeadsKv << ", \"D\": "
+          << kHeadDim << "}}\n";
     }
     return 0;
 }

@@ -122,6 +122,9 @@ _SIGS = [
     ("sca_pkv_destroy", None, [c_vp]),
     ("sca_pkv_append", ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
     ("sca_pkv_append_batch", ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
+    ("sca_pkv_reserve", ctypes.c_int, [c_vp, c_i64, c_i64, c_vp]),
+    ("sca_pkv_reserve_batch", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
+    ("sca_pkv_write_layer", ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_vp]),
     ("sca_pkv_reset", ctypes.c_int, [c_vp, c_i64, c_vp]),
     ("sca_pkv_sync", ctypes.c_int, [c_vp, c_vp]),
     ("sca_pkv_force_sync", ctypes.c_int, [c_vp, c_vp]),
@@ -542,6 +545,16 @@ class PagedKVCache:
         ids = np.ascontiguousarray(np.asarray(seq_ids, dtype=np.int64))
         _raise(host_lib().sca_pkv_append_batch(self.h, ids.ctypes.data, ids.size, layer,
                                                k_new.handle, v_new.handle, stream))
+
+    def reserve(self, seq, num_tokens, stream=None):
+        _raise(host_lib().sca_pkv_reserve(self.h, seq, num_tokens, stream))
+
+    def reserve_batch(self, seq_ids, stream=None):
+        ids = np.ascontiguousarray(np.asarray(seq_ids, dtype=np.int64))
+        _raise(host_lib().sca_pkv_reserve_batch(self.h, ids.ctypes.data, ids.size, stream))
+
+    def write_layer(self, layer, k_new: Tensor, v_new: Tensor, stream=None):
+        _raise(host_lib().sca_pkv_write_layer(self.h, layer, k_new.handle, v_new.handle, stream))
 
     def reset_seq(self, seq, stream=None):
         _raise(host_lib().sca_pkv_reset(self.h, seq, stream))

@@ -334,6 +334,20 @@ int sca_pkv_append_batch(ScaPagedKV* c, const int64_t* seq_ids, int64_t num_entr
     return Check(P(c).AppendTokensBatch(seq_ids, num_entries, layer, T(k_new), T(v_new),
                                         StreamArg(stream, &holder)));
 }
+int sca_pkv_reserve(ScaPagedKV* c, int64_t seq_id, int64_t num_tokens, void* stream) {
+    sci::Stream holder;
+    return Check(P(c).ReserveTokens(seq_id, num_tokens, StreamArg(stream, &holder)));
+}
+int sca_pkv_reserve_batch(ScaPagedKV* c, const int64_t* seq_ids, int64_t num_entries,
+                          void* stream) {
+    sci::Stream holder;
+    return Check(P(c).ReserveTokensBatch(seq_ids, num_entries, StreamArg(stream, &holder)));
+}
+int sca_pkv_write_layer(ScaPagedKV* c, int64_t layer, const ScaTensor* k_new,
+                        const ScaTensor* v_new, void* stream) {
+    sci::Stream holder;
+    return Check(P(c).WriteReservedLayer(layer, T(k_new), T(v_new), StreamArg(stream, &holder)));
+}
 int sca_pkv_reset(ScaPagedKV* c, int64_t seq_id, void* stream) {
     sci::Stream holder;
     return Check(P(c).ResetSeq(seq_id, StreamArg(stream, &holder)));

@@ -45,6 +45,7 @@ PagedKVCache::PagedKVCache(PagedKVCache&& o) noexcept
       page_table_device_(std::move(o.page_table_device_)),
       slot_mapping_device_(std::move(o.slot_mapping_device_)),
       slot_mapping_capacity_(o.slot_mapping_capacity_),
+      reserved_tokens_(o.reserved_tokens_),
       pairs_device_(std::move(o.pairs_device_)),
       pairs_capacity_(o.pairs_capacity_),
       staging_host_(o.staging_host_),
@@ -73,6 +74,7 @@ PagedKVCache& PagedKVCache::operator=(PagedKVCache&& o) noexcept {
         page_table_device_ = std::move(o.page_table_device_);
         slot_mapping_device_ = std::move(o.slot_mapping_device_);
         slot_mapping_capacity_ = o.slot_mapping_capacity_;
+        reserved_tokens_ = o.reserved_tokens_;
         pairs_device_ = std::move(o.pairs_device_);
         pairs_capacity_ = o.pairs_capacity_;
         staging_host_ = o.staging_host_;
@@ -201,6 +203,24 @@ sci::Status PagedKVCache::AppendTokens(int64_t seq_id, int64_t layer, const sci:
     if (num_new <= 0) {
         return MakeStatus(AttnStatusCode::kShapeMismatch, "PagedKVCache::AppendTokens: 0 tokens");
     }
+    const int64_t current_len = seq_lengths_[static_cast<size_t>(seq_id)];
+    sci::Status st = ReserveSlots(seq_id, num_new, "PagedKVCache::AppendTokens", stream);
+    if (!st.ok()) return st;
+    st = storage_.Append(layer, k_new, v_new,
+                         static_cast<const int32_t*>(slot_mapping_device_.data()), num_new, stream);
+    if (!st.ok()) return st;  // pages stay attached; ResetSeq recovers
+    seq_lengths_[static_cast<size_t>(seq_id)] = current_len + num_new;
+    ++revision_;
+    ++num_appends_;
+    return sci::Status::Ok();
+}
+
+// Pages for num_new more tokens of seq_id (all or nothing), the row's new tail, and the slots of
+// the tokens uploaded to slot_mapping_device_ on the stream. Lengths and the revision are left to
+// the caller. `who` names the entry point in the capacity message.
+sci::Status PagedKVCache::ReserveSlots(int64_t seq_id, int64_t num_new, const char* who,
+                                       sci::Stream* stream) {
+    reserved_tokens_ = 0;  // the slot buffer is about to hold this call's slots
     const size_t sid = static_cast<size_t>(seq_id);
     std::vector<int32_t>& owned = seq_blocks_[sid];
     const int64_t current_len = seq_lengths_[sid];
@@ -212,8 +232,8 @@ sci::Status PagedKVCache::AppendTokens(int64_t seq_id, int64_t layer, const sci:
         sci::Result<std::vector<int32_t>> got = blocks_.Allocate(missing);
         if (!got.ok()) {
             return MakeStatus(AttnStatusCode::kKVCapacityExceeded,
-                              "PagedKVCache::AppendTokens seq=" + std::to_string(seq_id) +
-                                  " needs " + std::to_string(missing) + " more blocks but only " +
+                              std::string(who) + " seq=" + std::to_string(seq_id) + " needs " +
+                                  std::to_string(missing) + " more blocks but only " +
                                   std::to_string(blocks_.NumFreeBlocks()) + " are free");
         }
         fresh = std::move(*got);
@@ -257,15 +277,7 @@ sci::Status PagedKVCache::AppendTokens(int64_t seq_id, int64_t layer, const sci:
                              static_cast<size_t>(num_new) * sizeof(int32_t), SCA_COPY_H2D, s),
         "PagedKVCache slot upload");
     if (st.ok()) st = StagingSubmitted(s, stream == nullptr);
-    if (!st.ok()) return st;
-
-    st = storage_.Append(layer, k_new, v_new,
-                         static_cast<const int32_t*>(slot_mapping_device_.data()), num_new, stream);
-    if (!st.ok()) return st;  // pages stay attached; ResetSeq recovers
-    seq_lengths_[sid] = current_len + num_new;
-    ++revision_;
-    ++num_appends_;
-    return sci::Status::Ok();
+    return st;
 }
 
 sci::Status PagedKVCache::AppendTokensBatch(const int64_t* seq_ids, int64_t num_entries,
@@ -280,42 +292,62 @@ sci::Status PagedKVCache::AppendTokensBatch(const int64_t* seq_ids, int64_t num_
                           "PagedKVCache::AppendTokensBatch layer=" + std::to_string(layer) +
                               " out of range [0," + std::to_string(cfg_.num_layers) + ")");
     }
-    if (k_new.ndims() != 3 || v_new.ndims() != 3 || k_new.dim(0) != num_entries ||
-        v_new.dim(0) != num_entries) {
+    const sci::Status shape = CheckTokenRows(k_new, v_new, num_entries,
+                                             "PagedKVCache::AppendTokensBatch");
+    if (!shape.ok()) return shape;
+    const sci::Status st = ReserveBatchSlots(seq_ids, num_entries,
+                                             "PagedKVCache::AppendTokensBatch", stream);
+    if (!st.ok()) return st;
+    reserved_tokens_ = 0;
+    return storage_.Append(layer, k_new, v_new,
+                           static_cast<const int32_t*>(slot_mapping_device_.data()), num_entries,
+                           stream);
+}
+
+// k_new / v_new are [rows, num_kv_heads, head_dim] tensors of the cache's dtype.
+sci::Status PagedKVCache::CheckTokenRows(const sci::Tensor& k_new, const sci::Tensor& v_new,
+                                         int64_t rows, const char* who) const {
+    if (k_new.ndims() != 3 || v_new.ndims() != 3 || k_new.dim(0) != rows ||
+        v_new.dim(0) != rows) {
         return MakeStatus(AttnStatusCode::kShapeMismatch,
-                          "PagedKVCache::AppendTokensBatch expects [num_entries, n_kv_heads, "
-                          "head_dim] tensors with one token per sequence id");
+                          std::string(who) + " expects [num_entries, n_kv_heads, head_dim] "
+                                             "tensors with one token per sequence id");
     }
     if (k_new.dim(1) != cfg_.num_kv_heads || k_new.dim(2) != cfg_.head_dim ||
         v_new.dim(1) != cfg_.num_kv_heads || v_new.dim(2) != cfg_.head_dim ||
         k_new.dtype() != cfg_.dtype || v_new.dtype() != cfg_.dtype) {
         return MakeStatus(AttnStatusCode::kShapeMismatch,
-                          "PagedKVCache::AppendTokensBatch token shape differs from the cache's [" +
+                          std::string(who) + " token shape differs from the cache's [" +
                               std::to_string(cfg_.num_kv_heads) + ", " +
                               std::to_string(cfg_.head_dim) + "]");
     }
+    return sci::Status::Ok();
+}
+
+// Pages, rows, slots (uploaded), lengths and revision for one token per entry of seq_ids, in
+// order, exactly as one AppendTokens call per entry would leave them; all or nothing.
+sci::Status PagedKVCache::ReserveBatchSlots(const int64_t* seq_ids, int64_t num_entries,
+                                            const char* who, sci::Stream* stream) {
+    reserved_tokens_ = 0;
     // Pages the whole batch needs, before anything changes.
     std::vector<int64_t> lens;   // running lengths of the sequences touched, by first appearance
     std::vector<int64_t> owned;  // their page counts
-    std::vector<int64_t> index(static_cast<size_t>(num_entries));
+    std::vector<int64_t> first(static_cast<size_t>(cfg_.max_num_seqs), -1);  // by sequence id
     int64_t missing = 0;
     for (int64_t i = 0; i < num_entries; ++i) {
         const int64_t id = seq_ids[i];
         if (id < 0 || id >= cfg_.max_num_seqs) {
             return MakeStatus(AttnStatusCode::kShapeMismatch,
-                              "PagedKVCache::AppendTokensBatch seq_id=" + std::to_string(id) +
+                              std::string(who) + " seq_id=" + std::to_string(id) +
                                   " out of range [0," + std::to_string(cfg_.max_num_seqs) + ")");
         }
-        int64_t k = 0;
-        while (k < i && seq_ids[k] != id) ++k;
-        if (k == i) {
-            index[static_cast<size_t>(i)] = static_cast<int64_t>(lens.size());
+        int64_t& slot = first[static_cast<size_t>(id)];
+        if (slot < 0) {
+            slot = static_cast<int64_t>(lens.size());
             lens.push_back(seq_lengths_[static_cast<size_t>(id)]);
             owned.push_back(static_cast<int64_t>(seq_blocks_[static_cast<size_t>(id)].size()));
-        } else {
-            index[static_cast<size_t>(i)] = index[static_cast<size_t>(k)];
         }
-        const size_t u = static_cast<size_t>(index[static_cast<size_t>(i)]);
+        const size_t u = static_cast<size_t>(slot);
         const int64_t needed = (lens[u] + 1 + cfg_.block_size - 1) / cfg_.block_size;
         if (needed > owned[u]) {
             missing += needed - owned[u];
@@ -323,7 +355,7 @@ sci::Status PagedKVCache::AppendTokensBatch(const int64_t* seq_ids, int64_t num_
         }
         if (needed > max_blocks_per_seq_) {
             return MakeStatus(AttnStatusCode::kKVCapacityExceeded,
-                              "PagedKVCache::AppendTokensBatch seq=" + std::to_string(id) +
+                              std::string(who) + " seq=" + std::to_string(id) +
                                   " would exceed " + std::to_string(max_blocks_per_seq_) +
                                   " pages");
         }
@@ -331,7 +363,7 @@ sci::Status PagedKVCache::AppendTokensBatch(const int64_t* seq_ids, int64_t num_
     }
     if (missing > blocks_.NumFreeBlocks()) {
         return MakeStatus(AttnStatusCode::kKVCapacityExceeded,
-                          "PagedKVCache::AppendTokensBatch needs " + std::to_string(missing) +
+                          std::string(who) + " needs " + std::to_string(missing) +
                               " more blocks but only " + std::to_string(blocks_.NumFreeBlocks()) +
                               " are free");
     }
@@ -384,13 +416,67 @@ sci::Status PagedKVCache::AppendTokensBatch(const int64_t* seq_ids, int64_t num_
                              static_cast<size_t>(num_entries) * sizeof(int32_t), SCA_COPY_H2D, s),
         "PagedKVCache batch slot upload");
     if (st.ok()) st = StagingSubmitted(s, stream == nullptr);
-    if (!st.ok()) return st;
-    return storage_.Append(layer, k_new, v_new,
-                           static_cast<const int32_t*>(slot_mapping_device_.data()), num_entries,
-                           stream);
+    return st;
 }
 
+// ---- multi-layer appends -----------------------------------------------------------------------
+
+sci::Status PagedKVCache::ReserveTokens(int64_t seq_id, int64_t num_tokens, sci::Stream* stream) {
+    reserved_tokens_ = 0;
+    if (seq_id < 0 || seq_id >= cfg_.max_num_seqs) {
+        return MakeStatus(AttnStatusCode::kShapeMismatch,
+                          "PagedKVCache::ReserveTokens seq_id=" + std::to_string(seq_id) +
+                              " out of range [0," + std::to_string(cfg_.max_num_seqs) + ")");
+    }
+    if (num_tokens <= 0) {
+        return MakeStatus(AttnStatusCode::kShapeMismatch, "PagedKVCache::ReserveTokens: 0 tokens");
+    }
+    const sci::Status st = ReserveSlots(seq_id, num_tokens, "PagedKVCache::ReserveTokens", stream);
+    if (!st.ok()) return st;
+    seq_lengths_[static_cast<size_t>(seq_id)] += num_tokens;
+    ++revision_;
+    ++num_appends_;
+    reserved_tokens_ = num_tokens;
+    return sci::Status::Ok();
+}
+
+sci::Status PagedKVCache::ReserveTokensBatch(const int64_t* seq_ids, int64_t num_entries,
+                                             sci::Stream* stream) {
+    reserved_tokens_ = 0;
+    if (seq_ids == nullptr || num_entries <= 0) {
+        return MakeStatus(AttnStatusCode::kShapeMismatch,
+                          "PagedKVCache::ReserveTokensBatch needs at least one sequence id");
+    }
+    const sci::Status st =
+        ReserveBatchSlots(seq_ids, num_entries, "PagedKVCache::ReserveTokensBatch", stream);
+    if (!st.ok()) return st;
+    reserved_tokens_ = num_entries;
+    return sci::Status::Ok();
+}
+
+sci::Status PagedKVCache::WriteReservedLayer(int64_t layer, const sci::Tensor& k_new,
+                                             const sci::Tensor& v_new, sci::Stream* stream) {
+    if (reserved_tokens_ <= 0) {
+        return MakeStatus(AttnStatusCode::kShapeMismatch,
+                          "PagedKVCache::WriteReservedLayer: no reservation (call ReserveTokens or "
+                          "ReserveTokensBatch first)");
+    }
+    if (layer < 0 || layer >= cfg_.num_layers) {
+        return MakeStatus(AttnStatusCode::kShapeMismatch,
+                          "PagedKVCache::WriteReservedLayer layer=" + std::to_string(layer) +
+                              " out of range [0," + std::to_string(cfg_.num_layers) + ")");
+    }
+    const sci::Status shape =
+        CheckTokenRows(k_new, v_new, reserved_tokens_, "PagedKVCache::WriteReservedLayer");
+    if (!shape.ok()) return shape;
+    return storage_.Append(layer, k_new, v_new,
+                           static_cast<const int32_t*>(slot_mapping_device_.data()),
+                           reserved_tokens_, stream);
+}
+
+
 sci::Status PagedKVCache::ResetSeq(int64_t seq_id, sci::Stream* stream) {
+    reserved_tokens_ = 0;  // the slot buffer carries the page ids below
     if (seq_id < 0 || seq_id >= cfg_.max_num_seqs) {
         return MakeStatus(AttnStatusCode::kShapeMismatch,
                           "PagedKVCache::ResetSeq seq_id=" + std::to_string(seq_id) +

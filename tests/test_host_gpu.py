@@ -282,3 +282,72 @@ def test_serving_loop_paged_decode(hip, dtype):
                                              srv.v[s].transpose(1, 0, 2)[None], False)
             check_attention(out[s].reshape(-1, D), ref, dtype, f"step {step} seq {s}")
     srv.check_state()
+
+
+def test_reserved_multi_layer_appends(hip):
+    # ReserveTokens / ReserveTokensBatch leave the allocator state of the equivalent AppendTokens /
+    # AppendTokensBatch calls, and each WriteReservedLayer lands its rows in its own layer only.
+    rng = np.random.default_rng(21)
+    layers, seqs, bs, Hkv, D, dt = 3, 5, 8, 2, 64, "bf16"
+    cfg = H.KVCacheConfig(layers, Hkv, D, bs, 64, seqs, dt)
+    a, b = H.PagedKVCache(cfg), H.PagedKVCache(H.KVCacheConfig(1, Hkv, D, bs, 64, seqs, dt))
+    hist = [[np.zeros((0, Hkv, D), np.uint16) for _ in range(seqs)] for _ in range(layers)]
+    vhist = [[np.zeros((0, Hkv, D), np.uint16) for _ in range(seqs)] for _ in range(layers)]
+
+    def write_all(ids, n_rows, seed):
+        for layer in range(layers):
+            kb, _ = quantize(uniform((n_rows, Hkv, D), seed + 2 * layer), dt)
+            vb, _ = quantize(uniform((n_rows, Hkv, D), seed + 2 * layer + 1), dt)
+            a.write_layer(layer, tensor(kb, dt), tensor(vb, dt))
+            for i, s in enumerate(ids):
+                hist[layer][s] = np.concatenate([hist[layer][s], kb[i:i + 1]])
+                vhist[layer][s] = np.concatenate([vhist[layer][s], vb[i:i + 1]])
+        return kb, vb
+
+    z = lambda n: tensor(np.zeros((n, Hkv, D), np.uint16), dt)  # noqa: E731
+    # Prompts: one reservation per sequence, written layer by layer.
+    for s in range(seqs):
+        n = int(rng.integers(1, 30))
+        a.reserve(s, n)
+        write_all([s] * n, n, 1000 + 10 * s)
+        b.append_tokens(s, 0, z(n), z(n))
+    # Decode steps: one batch reservation (ids may repeat), then every layer.
+    for step in range(12):
+        ids = [int(x) for x in rng.integers(0, seqs, size=int(rng.integers(1, 7)))]
+        a.reserve_batch(ids)
+        write_all(ids, len(ids), 5000 + 10 * step)
+        b.append_batch(ids, 0, z(len(ids)), z(len(ids)))
+        assert np.array_equal(a.page_table_host(), b.page_table_host())
+        assert a.revision == b.revision
+        for s in range(seqs):
+            assert a.seq_length(s) == b.seq_length(s)
+        sa, sb = a.stats(), b.stats()
+        for key in ("used_blocks", "free_blocks", "num_appends", "num_resets"):
+            assert sa[key] == sb[key], key
+    pt = a.page_table_host()
+    for layer in range(layers):
+        for s in range(seqs):
+            n, L = a.logical_block_count(s), a.seq_length(s)
+            ids = tensor(pt[s, :n].copy(), "i32")
+            gk = a.gather(True, layer, ids.data_ptr, n).numpy().reshape(n * bs, Hkv, D)[:L]
+            gv = a.gather(False, layer, ids.data_ptr, n).numpy().reshape(n * bs, Hkv, D)[:L]
+            assert np.array_equal(gk, hist[layer][s]), (layer, s)
+            assert np.array_equal(gv, vhist[layer][s]), (layer, s)
+    # Misuse is rejected without touching the state.
+    before = (a.page_table_host().copy(), a.revision)
+    a.append_tokens(0, 0, z(1), z(1))  # ends the last reservation
+    b.append_tokens(0, 0, z(1), z(1))
+    with pytest.raises(H.ScaError):
+        a.write_layer(1, z(1), z(1))
+    a.reserve_batch([1, 2])
+    with pytest.raises(H.ScaError):
+        a.write_layer(1, z(3), z(3))  # rows differ from the reservation
+    with pytest.raises(H.ScaError):
+        a.write_layer(layers, z(2), z(2))
+    b.append_batch([1, 2], 0, z(2), z(2))
+    free = a.stats()["free_blocks"]
+    with pytest.raises(H.ScaError) as e:
+        a.reserve_batch(np.repeat([3], (free + 1) * bs + bs))
+    assert e.value.code == 2007
+    assert np.array_equal(a.page_table_host(), b.page_table_host()) and a.revision == b.revision
+    assert not np.array_equal(before[0], a.page_table_host()) or before[1] != a.revision
