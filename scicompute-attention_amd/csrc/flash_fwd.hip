@@ -1374,31 +1374,6 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
         for (int ks = 0; ks < G::KS; ++ks) acc = M::mma(a[ks], qf[ks], acc);
         return acc;
     };
-    auto pv_slot = [&](int slot, const uint32_t (&pw)[8]) {
-        const uint8_t* vbase = lds8 + slot * G::TILE_BYTES;
-        const vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-        const vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
-        vec8 va[G::DT][2];
-#pragma unroll
-        for (int dt = 0; dt < G::DT; ++dt) {
-#pragma unroll
-            for (int ps = 0; ps < 2; ++ps) {
-                const uint2 lo = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps) * ROW_BYTES);
-                const uint2 hi = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps + 8) * ROW_BYTES);
-                va[dt][ps] = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-            }
-        }
-#pragma unroll
-        for (int dt = 0; dt < G::DT; ++dt) {
-            o[dt] = M::mma(va[dt][0], pb0, o[dt]);
-            o[dt] = M::mma(va[dt][1], pb1, o[dt]);
-        }
-#pragma unroll
-        for (int dt = 0; dt < G::DT; dt += 2) {
-            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
-        }
-    };
 
     // Key tiles [kb, ke) of row tile qt into the running state (o, rs.m, rs.l).
     auto run_keys = [&](int qt, int kb, int ke, int n_plain) {
