@@ -236,6 +236,15 @@ SCA_HIP_API int64_t sca_hip_decode_partial_elements(int64_t batch, int64_t num_h
                                                     int64_t num_splits, int64_t head_dim);
 SCA_HIP_API int sca_hip_decode_splitk(const sca_decode_params* params, void* stream);
 SCA_HIP_API int sca_hip_decode_splitk_paged(const sca_decode_params* params, void* stream);
+/* Allocation-free variant of sca_hip_decode_splitk (contiguous or paged, as page_table says).
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). partial_m/l/o
+ * and batch_order must be NULL: the split partials (at most 32 MiB:
+ * 4*sca_hip_decode_partial_elements(...) bytes) and the ranking scratch live in a static device
+ * array, one per GPU, held until the process ends. Larger split counts fail with
+ * SCA_E_WORKSPACE. Every call on one GPU shares that array: calls that overlap on one GPU (on
+ * different streams) race; calls ordered on one stream are safe. */
+SCA_HIP_API int sca_hip_decode_splitk_noalloc(const sca_decode_params* params, void* stream);
 
 /* ------------------------------------------------------------------------------------------- */
 /* KV cache data movement over the block-major layout [num_blocks][block_size][H_kv][D]         */

@@ -1065,6 +1065,52 @@ int ValidateDecode(const sca_decode_params* p, bool paged) {
     return 0;
 }
 
+// ---- allocation-free variant: the split partials and the ranking scratch live in a static
+// device array instead of caller memory ---------------------------------------------------------
+
+constexpr int64_t kNoAllocPartialBytes = int64_t{32} << 20;        // split-K partials
+constexpr int64_t kNoAllocOrderBytes = int64_t{2} * kMaxOrderedBatch * 4;  // batch_order
+constexpr int kNoAllocMaxDevices = 64;
+
+}  // namespace
+}  // namespace sca_hip
+
+// One copy per GPU, held until the process ends. Its host-side name is not a device address:
+// kernels receive the per-device address from hipGetSymbolAddress instead.
+static __device__ __align__(256) unsigned char
+    scratch[sca_hip::kNoAllocPartialBytes + sca_hip::kNoAllocOrderBytes];
+
+namespace sca_hip {
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per device.
+int NoAllocScratch(unsigned char** out) {
+    int dev = 0;
+    int rc = FromHip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc != 0) return rc;
+    if (dev < 0 || dev >= kNoAllocMaxDevices) {
+        return SetError(SCA_E_DEVICE_CAPABILITY,
+                        "decode (no-alloc): device " + std::to_string(dev) + " beyond the table");
+    }
+    static std::atomic<unsigned char*> ptrs[kNoAllocMaxDevices];
+    static std::mutex mu;
+    unsigned char* ptr = ptrs[dev].load(std::memory_order_acquire);
+    if (ptr == nullptr) {
+        std::lock_guard<std::mutex> lock(mu);
+        ptr = ptrs[dev].load(std::memory_order_relaxed);
+        if (ptr == nullptr) {
+            void* addr = nullptr;
+            rc = FromHip(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)),
+                         "hipGetSymbolAddress(scratch)");
+            if (rc != 0) return rc;
+            ptr = static_cast<unsigned char*>(addr);
+            ptrs[dev].store(ptr, std::memory_order_release);
+        }
+    }
+    *out = ptr;
+    return 0;
+}
+
 }  // namespace
 }  // namespace sca_hip
 
@@ -1099,6 +1145,47 @@ int sca_hip_decode_splitk_paged(const sca_decode_params* params, void* stream) {
     int rc = sca_hip::ValidateDecode(params, /*paged=*/true);
     if (rc != 0) return rc;
     return sca_hip_decode_splitk(params, stream);
+}
+
+int sca_hip_decode_splitk_noalloc(const sca_decode_params* params, void* stream) {
+    if (params == nullptr) return SetError(SCA_E_SHAPE_MISMATCH, "decode (no-alloc): null params");
+    if (params->partial_m != nullptr || params->partial_l != nullptr ||
+        params->partial_o != nullptr || params->batch_order != nullptr) {
+        return SetError(SCA_E_WORKSPACE,
+                        "decode (no-alloc): partial_m/l/o and batch_order must be NULL (the "
+                        "library's static scratch holds them)");
+    }
+    sca_decode_params p = *params;
+    if (p.batch < 1 || p.batch > 65535 || p.num_heads < 1 || p.num_heads > 65535 ||
+        p.num_splits < 1 || p.num_splits > 65535 || p.head_dim < 1 || p.head_dim > 256) {
+        return SetError(SCA_E_SHAPE_MISMATCH,
+                        "decode (no-alloc): batch, num_heads and num_splits must be in "
+                        "[1, 65535] and head_dim in [1, 256]");
+    }
+    if (p.num_splits > 1) {
+        const int64_t elems = p.batch * p.num_heads * p.num_splits;
+        const int64_t bytes = elems * (2 + p.head_dim) * 4;
+        if (bytes > sca_hip::kNoAllocPartialBytes) {
+            return SetError(SCA_E_WORKSPACE,
+                            "decode (no-alloc): the split partials need " + std::to_string(bytes) +
+                                " bytes, more than the static scratch's " +
+                                std::to_string(sca_hip::kNoAllocPartialBytes));
+        }
+    }
+    unsigned char* base = nullptr;
+    int rc = sca_hip::NoAllocScratch(&base);
+    if (rc != 0) return rc;
+    if (p.num_splits > 1) {
+        const int64_t elems = p.batch * p.num_heads * p.num_splits;
+        float* f = reinterpret_cast<float*>(base);
+        p.partial_m = f;
+        p.partial_l = f + elems;
+        p.partial_o = f + 2 * elems;
+    }
+    // Every split writes its partials and the ranking kernel writes every order entry, so
+    // nothing in the scratch needs clearing between calls.
+    p.batch_order = reinterpret_cast<int32_t*>(base + sca_hip::kNoAllocPartialBytes);
+    return sca_hip_decode_splitk(&p, stream);
 }
 
 }  // extern "C"

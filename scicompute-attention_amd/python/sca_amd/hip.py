@@ -137,6 +137,7 @@ def hip_lib() -> ctypes.CDLL:
     lib.sca_hip_decode_partial_elements.restype = c_i64
     lib.sca_hip_decode_splitk.argtypes = [ctypes.POINTER(DecodeParams), c_vp]
     lib.sca_hip_decode_splitk_paged.argtypes = [ctypes.POINTER(DecodeParams), c_vp]
+    lib.sca_hip_decode_splitk_noalloc.argtypes = [ctypes.POINTER(DecodeParams), c_vp]
     lib.sca_hip_kv_append.argtypes = [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
                                       ctypes.POINTER(KvShape), c_i64, c_vp]
     lib.sca_hip_kv_reset_blocks.argtypes = [c_vp, c_vp, c_vp, c_i64, ctypes.POINTER(KvShape),
@@ -271,3 +272,8 @@ def decode_splitk(params: DecodeParams, stream=None) -> None:
 
 def decode_splitk_paged(params: DecodeParams, stream=None) -> None:
     check(hip_lib().sca_hip_decode_splitk_paged(ctypes.byref(params), stream))
+
+
+def decode_splitk_noalloc(params: DecodeParams, stream=None) -> None:
+    """The allocation-free decode entry point: partial_m/l/o and batch_order must be None."""
+    check(hip_lib().sca_hip_decode_splitk_noalloc(ctypes.byref(params), stream))
