@@ -395,6 +395,54 @@ def bench_paged_host(steps):
 
 
 # ---- copy calibration ------------------------------------------------------------------------------
+def bench_page_probe(steps, warmup, num_seqs=64, bs=16, Hkv=8, D=128, lo=512, hi=16384):
+    """The paged decode's read pattern alone (lib/libsca_calib.so): C5's starting pool (same
+    seed, lengths, permuted page table and split count as the paged leg), K and V head slices
+    of every page read once, nothing computed. Reported per in-flight depth (32-token tiles per
+    wave, 16 KB each); the best is the practical ceiling for the paged decode kernel. Sequences
+    run longest first, as the decode kernel runs a ragged batch."""
+    import ctypes
+    rng = np.random.default_rng(5005)
+    lengths = rng.integers(lo, hi + 1, size=num_seqs).astype(np.int64)
+    need = (lengths + bs - 1) // bs
+    num_blocks = int(need.sum()) + 64
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    max_blocks = int(need.max())
+    table = np.full((num_seqs, max_blocks), -1, np.int32)
+    pos = 0
+    for s in range(num_seqs):
+        table[s, : need[s]] = perm[pos: pos + need[s]]
+        pos += need[s]
+    splits = dispatcher_splits(num_seqs, 32, Hkv, num_blocks * bs, D)
+    # Longest sequences first, as the decode kernel schedules a ragged batch.
+    order = np.argsort(-lengths, kind="stable")
+    table, lengths = np.ascontiguousarray(table[order]), lengths[order]
+    page = bs * Hkv * D * 2
+    dk = H.DeviceBuffer(num_blocks * page)
+    dv = H.DeviceBuffer(num_blocks * page)
+    dt = H.DeviceBuffer.from_array(table)
+    dl = H.DeviceBuffer.from_array(lengths.astype(np.int32))
+    sink = H.DeviceBuffer(64)
+    lib = ctypes.CDLL(os.path.join(sca_amd.hip.LIB_DIR, "libsca_calib.so"))
+    c_vp, c_int = ctypes.c_void_p, ctypes.c_int
+    lib.sca_calib_page_read.argtypes = [c_vp, c_vp, c_vp, c_vp] + [c_int] * 6 + [c_vp, c_vp]
+    nbytes = int(lengths.sum()) * Hkv * D * 2 * 2
+    # mode 0: K and V to registers, 4 rows x 256 B per load; mode 3: the decode kernel's own
+    # pattern (V through LDS with global_load_lds, K as MFMA fragments of 16 rows x 64 B).
+    variants = [(0, d) for d in (1, 2, 3, 4)] + [(3, d) for d in (1, 2)]
+    out = {"bytes_read": nbytes, "splits": splits, "runs": {}}
+    for mode, depth in variants:
+        ms = time_launches(lambda: H.check(lib.sca_calib_page_read(
+            dk.ptr, dv.ptr, dt.ptr, dl.ptr, num_seqs, Hkv, max_blocks, splits, depth, mode,
+            sink.ptr, None)), steps, warmup)
+        out["runs"][f"mode{mode}_depth{depth}"] = {"ms": ms, "gbps": nbytes / (ms * 1e-3) / 1e9}
+    best = max((r for k, r in out["runs"].items() if k.startswith("mode0")), key=lambda r: r["gbps"])
+    own = max((r for k, r in out["runs"].items() if k.startswith("mode3")), key=lambda r: r["gbps"])
+    out["gbps"], out["ms"] = best["gbps"], best["ms"]
+    out["decode_pattern_gbps"] = own["gbps"]
+    return out
+
+
 def bench_copy(steps, warmup, mib=256):
     """A plain copy of known size (the block gather kernel over ids 0..n-1): the reference point
     that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes, and the practical HBM
@@ -528,12 +576,12 @@ def main():
     ap.add_argument("--prewarm", type=float, default=0.5,
                     help="seconds of untimed launches of each leg's own work before it is timed")
     ap.add_argument("--only", default="all",
-                    help="comma list of prefill, gqa, paged, paged_host, decode, copy "
-                         "(default: all but copy)")
+                    help="comma list of prefill, gqa, paged, paged_host, decode, copy, "
+                         "page_probe (default: all but copy and page_probe)")
     args = ap.parse_args()
     parts = ({"prefill", "gqa", "paged", "paged_host", "decode"} if args.only == "all"
              else set(args.only.split(",")))
-    unknown = parts - {"prefill", "gqa", "paged", "paged_host", "decode", "copy"}
+    unknown = parts - {"prefill", "gqa", "paged", "paged_host", "decode", "copy", "page_probe"}
     if unknown:
         ap.error(f"unknown --only part(s): {sorted(unknown)}")
     if args.gpus != 1:
@@ -559,6 +607,8 @@ def main():
         res["c4_decode"] = bench_decode(args.steps, args.warmup, prewarm_s=args.prewarm)
     if "copy" in parts:
         res["copy"] = bench_copy(args.steps, args.warmup)
+    if "page_probe" in parts:
+        res["page_probe"] = bench_page_probe(args.steps, args.warmup)
 
     line = {
         "metric": "prefill TFLOP/s (causal S=4096) + paged decode HBM GB/s, 1xMI355X",
@@ -620,6 +670,17 @@ def main():
     if "copy" in res:
         line["copy_calibration"] = {k: round(v, 4) if isinstance(v, float) else v
                                     for k, v in res["copy"].items()}
+    if "page_probe" in res:
+        pr = res["page_probe"]
+        line["page_read_calibration"] = {
+            "gbps": round(pr["gbps"], 1), "ms": round(pr["ms"], 4),
+            "decode_pattern_gbps": round(pr["decode_pattern_gbps"], 1), "splits": pr["splits"],
+            "bytes_read": pr["bytes_read"],
+            "runs": {k: {"gbps": round(r["gbps"], 1), "ms": round(r["ms"], 4)}
+                     for k, r in pr["runs"].items()},
+            "what": "C5's starting K/V pages read once in the paged decode's order, nothing "
+                    "computed (lib/libsca_calib.so): gbps = best coalesced pattern, "
+                    "decode_pattern_gbps = the decode kernel's own load pattern"}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))

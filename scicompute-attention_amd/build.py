@@ -2,6 +2,7 @@
 
 Outputs (all under ``scicompute-attention_amd/lib/``):
   * ``libsca_hip.so``  - gfx950 HIP kernels + their C ABI (include/sca_hip.h)
+  * ``libsca_calib.so`` - calibration kernels timed by bench.py (not part of the library)
   * ``libsca_host.so`` - the C++ host layer (sca:: API, dispatcher, KV cache) + the ctypes-facing
     C ABI (include/sca_capi.h); links libsca_hip.so
 
@@ -146,11 +147,22 @@ def build_examples() -> list[str]:
     return outs
 
 
+def build_calib() -> str:
+    """Calibration kernels for bench.py (calib/*.hip) in lib/libsca_calib.so; not part of the
+    attention library."""
+    out = os.path.join(LIB_DIR, "libsca_calib.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", *sorted(glob.glob(os.path.join(PKG_DIR, "calib", "*.hip"))),
+          "-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
 def build(workers: int | None = None) -> list[str]:
     workers = workers or min(8, os.cpu_count() or 4)
     if os.path.isdir(OBJ_DIR):
         shutil.rmtree(OBJ_DIR)
-    outputs = [build_hip(workers)]
+    outputs = [build_hip(workers), build_calib()]
     if glob.glob(os.path.join(SRC_DIR, "**", "*.cpp"), recursive=True):
         outputs.append(build_host(workers))
         if os.path.exists(os.path.join(REPO_DIR, "tests", "cpp", "test_host_api.cpp")):
