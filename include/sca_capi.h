@@ -171,6 +171,11 @@ SCA_CAPI int sca_pkv_reserve_batch(ScaPagedKV* c, const int64_t* seq_ids, int64_
                                    void* stream);
 SCA_CAPI int sca_pkv_write_layer(ScaPagedKV* c, int64_t layer, const ScaTensor* k_new,
                                  const ScaTensor* v_new, void* stream);
+/* One call for all layers (sca::PagedKVCache::AppendTokensBatchAllLayers): k_layers/v_layers
+ * are [num_layers, num_entries, num_kv_heads, head_dim]. */
+SCA_CAPI int sca_pkv_append_batch_all_layers(ScaPagedKV* c, const int64_t* seq_ids,
+                                             int64_t num_entries, const ScaTensor* k_layers,
+                                             const ScaTensor* v_layers, void* stream);
 SCA_CAPI int sca_pkv_reset(ScaPagedKV* c, int64_t seq_id, void* stream);
 SCA_CAPI int sca_pkv_sync(ScaPagedKV* c, void* stream);
 SCA_CAPI int sca_pkv_force_sync(ScaPagedKV* c, void* stream);

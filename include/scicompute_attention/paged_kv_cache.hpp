@@ -73,6 +73,12 @@ public:
     sci::Status WriteReservedLayer(int64_t layer, const sci::Tensor& k_new,
                                    const sci::Tensor& v_new, sci::Stream* stream);
     int64_t ReservedTokens() const noexcept { return reserved_tokens_; }
+    // One call for all layers: k_layers / v_layers are [num_layers, num_entries, num_kv_heads,
+    // head_dim]; reserves one token per entry (ids may repeat, as in AppendTokensBatch) and writes
+    // every layer's rows. Shapes are checked before anything changes.
+    sci::Status AppendTokensBatchAllLayers(const int64_t* seq_ids, int64_t num_entries,
+                                           const sci::Tensor& k_layers,
+                                           const sci::Tensor& v_layers, sci::Stream* stream);
 
     // Zeroes the sequence's pages, returns them to the pool and clears its row.
     sci::Status ResetSeq(int64_t seq_id, sci::Stream* stream);

@@ -125,6 +125,7 @@ _SIGS = [
     ("sca_pkv_reserve", ctypes.c_int, [c_vp, c_i64, c_i64, c_vp]),
     ("sca_pkv_reserve_batch", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
     ("sca_pkv_write_layer", ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_vp]),
+    ("sca_pkv_append_batch_all_layers", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp]),
     ("sca_pkv_reset", ctypes.c_int, [c_vp, c_i64, c_vp]),
     ("sca_pkv_sync", ctypes.c_int, [c_vp, c_vp]),
     ("sca_pkv_force_sync", ctypes.c_int, [c_vp, c_vp]),
@@ -555,6 +556,11 @@ class PagedKVCache:
 
     def write_layer(self, layer, k_new: Tensor, v_new: Tensor, stream=None):
         _raise(host_lib().sca_pkv_write_layer(self.h, layer, k_new.handle, v_new.handle, stream))
+
+    def append_batch_all_layers(self, seq_ids, k_layers: Tensor, v_layers: Tensor, stream=None):
+        ids = np.ascontiguousarray(np.asarray(seq_ids, dtype=np.int64))
+        _raise(host_lib().sca_pkv_append_batch_all_layers(self.h, ids.ctypes.data, ids.size,
+                                                          k_layers.handle, v_layers.handle, stream))
 
     def reset_seq(self, seq, stream=None):
         _raise(host_lib().sca_pkv_reset(self.h, seq, stream))

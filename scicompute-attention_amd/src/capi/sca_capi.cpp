@@ -348,6 +348,13 @@ int sca_pkv_write_layer(ScaPagedKV* c, int64_t layer, const ScaTensor* k_new,
     sci::Stream holder;
     return Check(P(c).WriteReservedLayer(layer, T(k_new), T(v_new), StreamArg(stream, &holder)));
 }
+int sca_pkv_append_batch_all_layers(ScaPagedKV* c, const int64_t* seq_ids, int64_t num_entries,
+                                    const ScaTensor* k_layers, const ScaTensor* v_layers,
+                                    void* stream) {
+    sci::Stream holder;
+    return Check(P(c).AppendTokensBatchAllLayers(seq_ids, num_entries, T(k_layers), T(v_layers),
+                                                 StreamArg(stream, &holder)));
+}
 int sca_pkv_reset(ScaPagedKV* c, int64_t seq_id, void* stream) {
     sci::Stream holder;
     return Check(P(c).ResetSeq(seq_id, StreamArg(stream, &holder)));

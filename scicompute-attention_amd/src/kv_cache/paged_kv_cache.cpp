@@ -475,6 +475,45 @@ sci::Status PagedKVCache::WriteReservedLayer(int64_t layer, const sci::Tensor& k
 }
 
 
+sci::Status PagedKVCache::AppendTokensBatchAllLayers(const int64_t* seq_ids, int64_t num_entries,
+                                                     const sci::Tensor& k_layers,
+                                                     const sci::Tensor& v_layers,
+                                                     sci::Stream* stream) {
+    const char* who = "PagedKVCache::AppendTokensBatchAllLayers";
+    if (seq_ids == nullptr || num_entries <= 0) {
+        return MakeStatus(AttnStatusCode::kShapeMismatch,
+                          std::string(who) + " needs at least one sequence id");
+    }
+    for (const sci::Tensor* t : {&k_layers, &v_layers}) {
+        if (t->ndims() != 4 || t->dim(0) != cfg_.num_layers || t->dim(1) != num_entries ||
+            t->dim(2) != cfg_.num_kv_heads || t->dim(3) != cfg_.head_dim ||
+            t->dtype() != cfg_.dtype) {
+            return MakeStatus(AttnStatusCode::kShapeMismatch,
+                              std::string(who) + " expects [num_layers, num_entries, n_kv_heads, "
+                                                 "head_dim] = [" +
+                                  std::to_string(cfg_.num_layers) + ", " +
+                                  std::to_string(num_entries) + ", " +
+                                  std::to_string(cfg_.num_kv_heads) + ", " +
+                                  std::to_string(cfg_.head_dim) + "] tensors of the cache's dtype");
+        }
+    }
+    sci::Status st = ReserveBatchSlots(seq_ids, num_entries, who, stream);
+    if (!st.ok()) return st;
+    reserved_tokens_ = num_entries;
+    const int64_t layer_bytes = num_entries * cfg_.num_kv_heads * cfg_.head_dim *
+                                static_cast<int64_t>(sci::kDTypeSize(cfg_.dtype));
+    const sci::TensorShape rows({num_entries, cfg_.num_kv_heads, cfg_.head_dim});
+    for (int64_t layer = 0; layer < cfg_.num_layers; ++layer) {
+        const sci::Tensor k(rows, cfg_.dtype, k_layers.device(),
+                            static_cast<char*>(const_cast<void*>(k_layers.data())) + layer * layer_bytes);
+        const sci::Tensor v(rows, cfg_.dtype, v_layers.device(),
+                            static_cast<char*>(const_cast<void*>(v_layers.data())) + layer * layer_bytes);
+        st = WriteReservedLayer(layer, k, v, stream);
+        if (!st.ok()) return st;
+    }
+    return sci::Status::Ok();
+}
+
 sci::Status PagedKVCache::ResetSeq(int64_t seq_id, sci::Stream* stream) {
     reserved_tokens_ = 0;  // the slot buffer carries the page ids below
     if (seq_id < 0 || seq_id >= cfg_.max_num_seqs) {

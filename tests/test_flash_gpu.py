@@ -9,7 +9,10 @@ import numpy as np
 import pytest
 
 import oracle.oracle as orc
-from attn_util import (bhsd_to_bshd, check_attention, normal, quantize, run_flash, uniform)
+import sca_amd
+from sca_amd import hip as H
+from attn_util import (DTYPE_ID, bhsd_to_bshd, check_attention, normal, quantize, run_flash, to_float,
+                       uniform)
 
 pytestmark = pytest.mark.gpu
 
@@ -237,3 +240,45 @@ def test_varlen_one_launch(hip, D, causal):
     _varlen_case("f16", causal, lens_q, lens_kv, 8, 8, D, 61000 + D + int(causal))
     # GQA, bf16, S_kv > S_q (bottom-right diagonal per sequence)
     _varlen_case("bf16", causal, [96, 3, 257], [160, 40, 400], 8, 2, D, 62000 + D + int(causal))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_kv_extent_beyond_2gib_falls_back(hip, causal):
+    """K/V rows so far apart that a launch's K/V extent passes 2 GiB: the DMA-based kernels
+    address K/V with 32-bit buffer offsets, so the launcher takes the register kernel instead,
+    whose results must match the oracle like any other."""
+    Sq = Skv = 1024
+    D, dtype = 128, "f16"
+    # (Skv + 256) rows of this stride exceed 2^31 bytes (the pair kernel's check; the wide
+    # kernel's, with 512 rows of overrun, too).
+    row = ((1 << 31) // (2 * (Skv + 256)) + 8) // 8 * 8
+    q = uniform((1, 1, Sq, D), 51)
+    k = uniform((1, 1, Skv, D), 52)
+    v = uniform((1, 1, Skv, D), 53)
+    (qb, qd), (kb, kd), (vb, vd) = quantize(q, dtype), quantize(k, dtype), quantize(v, dtype)
+    nbytes = ((Skv - 1) * row + D) * 2
+    L = sca_amd.hip_lib()
+    dk, dv = H.DeviceBuffer(nbytes), H.DeviceBuffer(nbytes)
+    for dst, src in ((dk, kb), (dv, vb)):
+        rows = np.ascontiguousarray(src.reshape(Skv, D))
+        for j in range(Skv):
+            H.check(L.sca_hip_memcpy(dst.ptr + j * row * 2, rows[j].ctypes.data, D * 2, H.COPY_H2D))
+    dq = H.DeviceBuffer.from_array(qb)
+    dout = H.DeviceBuffer(Sq * D * 2)
+    p = H.FlashParams()
+    p.q, p.k, p.v, p.out, p.lse = dq.ptr, dk.ptr, dv.ptr, dout.ptr, None
+    p.batch, p.num_heads, p.num_kv_heads = 1, 1, 1
+    p.seq_q, p.seq_kv, p.head_dim = Sq, Skv, D
+    p.q_sb, p.q_sh, p.q_ss = Sq * D, Sq * D, D
+    p.k_sb, p.k_sh, p.k_ss = Skv * row, Skv * row, row
+    p.v_sb, p.v_sh, p.v_ss = Skv * row, Skv * row, row
+    p.o_sb, p.o_sh, p.o_ss = Sq * D, Sq * D, D
+    p.scale = float(np.float32(1.0 / np.sqrt(np.float64(D))))
+    p.causal = 1 if causal else 0
+    p.dtype = DTYPE_ID[dtype]
+    p.diagonal = 0
+    H.flash_fwd(p)
+    sca_amd.synchronize()
+    out = to_float(dout.download(np.uint16), dtype).reshape(Sq, D)
+    ref, _ = orc.reference_attention(qd, kd, vd, causal)
+    check_attention(out, ref, dtype, f"2 GiB extent causal={causal}", abs_gate=True)

@@ -294,14 +294,21 @@ def test_reserved_multi_layer_appends(hip):
     hist = [[np.zeros((0, Hkv, D), np.uint16) for _ in range(seqs)] for _ in range(layers)]
     vhist = [[np.zeros((0, Hkv, D), np.uint16) for _ in range(seqs)] for _ in range(layers)]
 
+    # c gets the same tokens through the one-call form (every layer's rows stacked).
+    c = H.PagedKVCache(cfg)
+
     def write_all(ids, n_rows, seed):
+        ks, vs = [], []
         for layer in range(layers):
             kb, _ = quantize(uniform((n_rows, Hkv, D), seed + 2 * layer), dt)
             vb, _ = quantize(uniform((n_rows, Hkv, D), seed + 2 * layer + 1), dt)
             a.write_layer(layer, tensor(kb, dt), tensor(vb, dt))
+            ks.append(kb)
+            vs.append(vb)
             for i, s in enumerate(ids):
                 hist[layer][s] = np.concatenate([hist[layer][s], kb[i:i + 1]])
                 vhist[layer][s] = np.concatenate([vhist[layer][s], vb[i:i + 1]])
+        c.append_batch_all_layers(ids, tensor(np.stack(ks), dt), tensor(np.stack(vs), dt))
         return kb, vb
 
     z = lambda n: tensor(np.zeros((n, Hkv, D), np.uint16), dt)  # noqa: E731
@@ -325,14 +332,24 @@ def test_reserved_multi_layer_appends(hip):
         for key in ("used_blocks", "free_blocks", "num_appends", "num_resets"):
             assert sa[key] == sb[key], key
     pt = a.page_table_host()
+    # (Revisions differ by design: a batch counts one per entry, ReserveTokens one per call.)
+    assert np.array_equal(c.page_table_host(), pt)
     for layer in range(layers):
         for s in range(seqs):
             n, L = a.logical_block_count(s), a.seq_length(s)
+            assert c.seq_length(s) == L
             ids = tensor(pt[s, :n].copy(), "i32")
-            gk = a.gather(True, layer, ids.data_ptr, n).numpy().reshape(n * bs, Hkv, D)[:L]
-            gv = a.gather(False, layer, ids.data_ptr, n).numpy().reshape(n * bs, Hkv, D)[:L]
-            assert np.array_equal(gk, hist[layer][s]), (layer, s)
-            assert np.array_equal(gv, vhist[layer][s]), (layer, s)
+            for cache in (a, c):
+                gk = cache.gather(True, layer, ids.data_ptr, n).numpy().reshape(n * bs, Hkv, D)[:L]
+                gv = cache.gather(False, layer, ids.data_ptr, n).numpy().reshape(n * bs, Hkv, D)[:L]
+                assert np.array_equal(gk, hist[layer][s]), (layer, s)
+                assert np.array_equal(gv, vhist[layer][s]), (layer, s)
+    # The one-call form checks its shapes before anything changes.
+    before = (c.page_table_host().copy(), c.revision)
+    with pytest.raises(H.ScaError):
+        c.append_batch_all_layers([0, 1], tensor(np.zeros((layers - 1, 2, Hkv, D), np.uint16), dt),
+                                  tensor(np.zeros((layers - 1, 2, Hkv, D), np.uint16), dt))
+    assert np.array_equal(c.page_table_host(), before[0]) and c.revision == before[1]
     # Misuse is rejected without touching the state.
     before = (a.page_table_host().copy(), a.revision)
     a.append_tokens(0, 0, z(1), z(1))  # ends the last reservation
