@@ -1754,9 +1754,9 @@ __device__ __forceinline__ void SettleO(floatx16 (&o)[2][DT]) {
     }
 }
 
-template <typename E, int D, bool kCausal>
+template <typename E, int D, bool kCausal, bool kVarlen>
 __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel(
-    const sca_flash_params p, int num_q_tiles) {
+    const sca_flash_params p, int num_q_tiles, const VarlenArgs vl) {
     using G = WideGeom<D>;
     using M = Mfma<E>;
     using A = MfmaAsm<E>;
@@ -1780,11 +1780,22 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
     const int64_t b = bh / p.num_heads;
     const int64_t h = bh % p.num_heads;
     const int64_t h_kv = h / (p.num_heads / p.num_kv_heads);
-    // Causal: longest row tiles first.
-    const int qt = static_cast<int>(kCausal ? (num_q_tiles - 1 - tile_linear) : tile_linear);
-    const int seq_q = static_cast<int>(p.seq_q);
-    const int seq_kv = static_cast<int>(p.seq_kv);
-    const int diag = static_cast<int>(p.diagonal);
+    // Causal: longest row tiles first. A packed varlen launch takes the sequence and row tile of
+    // work entry tile_linear (the list is longest first); tok_*: the sequence's first token.
+    int qt = static_cast<int>(kCausal ? (num_q_tiles - 1 - tile_linear) : tile_linear);
+    int seq_q = static_cast<int>(p.seq_q);
+    int seq_kv = static_cast<int>(p.seq_kv);
+    int diag = static_cast<int>(p.diagonal);
+    int64_t tok_q = 0, tok_kv = 0;
+    if constexpr (kVarlen) {
+        const int seq = vl.tiles[2 * tile_linear];
+        qt = vl.tiles[2 * tile_linear + 1];
+        tok_q = vl.cu_q[seq];
+        tok_kv = vl.cu_kv[seq];
+        seq_q = vl.cu_q[seq + 1] - static_cast<int>(tok_q);
+        seq_kv = vl.cu_kv[seq + 1] - static_cast<int>(tok_kv);
+        diag = kCausal ? seq_kv - seq_q : 0;
+    }
     const float scale2 = p.scale * kLog2e;
     const float inv_scale2 = 1.0f / scale2;
     const int q0 = qt * BM;
@@ -1807,7 +1818,7 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
     for (int r = 0; r < G::RT; ++r) {
         const int row = row0 + 32 * r;
         const uint16_t* q_row = static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh +
-                                static_cast<int64_t>(row) * p.q_ss + 8 * hh;
+                                (tok_q + row) * p.q_ss + 8 * hh;
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) {
             uint4 raw = make_uint4(0, 0, 0, 0);
@@ -1818,9 +1829,9 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
 
     // ---- DMA (as in the DMA kernel: buffer resources bounded at the last row) ----
     const uint8_t* k_bytes = reinterpret_cast<const uint8_t*>(
-        static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh);
+        static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh + tok_kv * p.k_ss);
     const uint8_t* v_bytes = reinterpret_cast<const uint8_t*>(
-        static_cast<const uint16_t*>(p.v) + b * p.v_sb + h_kv * p.v_sh);
+        static_cast<const uint16_t*>(p.v) + b * p.v_sb + h_kv * p.v_sh + tok_kv * p.v_ss);
     const int k_row_bytes = static_cast<int>(p.k_ss) * 2;
     const int v_row_bytes = static_cast<int>(p.v_ss) * 2;
     const int k_records = (seq_kv - 1) * k_row_bytes + RB;
@@ -2276,7 +2287,7 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
         const int row = row0 + 32 * r;
         const bool row_ok = row < seq_q;
         uint16_t* out_row = static_cast<uint16_t*>(p.out) + b * p.o_sb + h * p.o_sh +
-                            static_cast<int64_t>(row) * p.o_ss;
+                            (tok_q + row) * p.o_ss;
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) {
 #pragma unroll
@@ -2318,11 +2329,12 @@ int LaunchFlashWide(const sca_flash_params& p, hipStream_t s) {
                                                 " workgroups exceeds the launch limit");
     }
     if (const int rc =
-            EnsureLdsLimit<&flash_fwd_wide_kernel<E, D, kCausal>>(G::LDS_BYTES, "flash LDS limit")) {
+            EnsureLdsLimit<&flash_fwd_wide_kernel<E, D, kCausal, false>>(G::LDS_BYTES, "flash LDS limit")) {
         return rc;
     }
-    hipLaunchKernelGGL((flash_fwd_wide_kernel<E, D, kCausal>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(G::THREADS), G::LDS_BYTES, s, p, static_cast<int>(num_q_tiles));
+    hipLaunchKernelGGL((flash_fwd_wide_kernel<E, D, kCausal, false>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(G::THREADS), G::LDS_BYTES, s, p,
+                       static_cast<int>(num_q_tiles), VarlenArgs{nullptr, nullptr, nullptr});
     return CheckLaunch("flash_fwd_wide_kernel", s);
 }
 
@@ -2470,11 +2482,26 @@ int LaunchForDim(const sca_flash_params& p, hipStream_t s) {
 
 bool Aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
+// Packed batches run the wide-row kernel. A measurement build reads SCA_FLASH_WIDE_VARLEN=0 to
+// run the 8-wave DMA kernel instead.
+bool UseWideVarlen() {
+#ifdef SCA_MEASUREMENT_BUILD
+    static const bool on = [] {
+        const char* env = std::getenv("SCA_FLASH_WIDE_VARLEN");
+        return env == nullptr || std::atoi(env) != 0;
+    }();
+    return on;
+#else
+    return true;
+#endif
+}
+
 // One launch over a packed batch: the 128-row geometry, one workgroup per (work entry, head).
 template <typename E, int D, bool kCausal>
 int LaunchFlashVarlen(const sca_flash_varlen_params& v, hipStream_t s) {
     using G = DmaGeom<D, 4, 2>;
-    const int64_t rows_k = v.max_seq_kv + 4 * G::BN;
+    // 32-bit buffer offsets: a sequence's rows plus the wide kernel's ring overrun must fit.
+    const int64_t rows_k = v.max_seq_kv + 8 * G::BN;
     if (rows_k * v.k_ss * 2 >= (1LL << 31) || rows_k * v.v_ss * 2 >= (1LL << 31)) {
         return SetError(SCA_E_SEQ_TOO_LONG, "flash varlen: a sequence of " +
                                                 std::to_string(v.max_seq_kv) +
@@ -2502,6 +2529,18 @@ int LaunchFlashVarlen(const sca_flash_varlen_params& v, hipStream_t s) {
     p.scale = v.scale;
     p.causal = v.causal;
     p.dtype = v.dtype;
+    if (UseWideVarlen()) {
+        using W = WideGeom<D>;
+        static_assert(W::BM == G::BM, "the work list's row tiles fit either kernel");
+        if (const int rc = EnsureLdsLimit<&flash_fwd_wide_kernel<E, D, kCausal, true>>(
+                W::LDS_BYTES, "flash LDS limit")) {
+            return rc;
+        }
+        hipLaunchKernelGGL((flash_fwd_wide_kernel<E, D, kCausal, true>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(W::THREADS), W::LDS_BYTES, s,
+                           p, 0, VarlenArgs{v.cu_seqlens_q, v.cu_seqlens_kv, v.tiles});
+        return CheckLaunch("flash_fwd_wide_kernel (varlen)", s);
+    }
     if (const int rc =
             EnsureLdsLimit<&flash_fwd_dma_kernel<E, D, 4, 2, kCausal, true>>(G::LDS_BYTES, "flash LDS limit")) {
         return rc;
