@@ -86,6 +86,9 @@ def test_causal_two_group_pairs(hip, sq, skv, D, dtype):
     (1, 8, 8, 1, 700, 128, "f16"),      # one query row far below the diagonal
     (1, 2, 1, 1473, 1473, 128, "f16"),  # 24 row tiles with a 1-row tail, 12 pairs
     (3, 4, 4, 130, 130, 64, "f16"),     # three tiles: one pair and a lone middle tile
+    (1, 2, 2, 2100, 2100, 128, "f16"),  # 33 tiles: the lone middle tile runs both phases alone
+    (1, 2, 1, 1500, 2000, 64, "bf16"),  # diagonal moved by 500 keys, long two-phase pairs
+    (1, 2, 2, 380, 380, 128, "bf16"),   # 6 tiles: pairs at the single/two-phase boundary
 ])
 def test_causal_two_group_pairs_shapes(hip, B, Hq, Hkv, sq, skv, D, dtype):
     _case(dtype, True, B, Hq, Hkv, sq, skv, D, 52000 + sq + skv + D, want_lse=True)
