@@ -69,6 +69,12 @@ def dispatcher_splits(batch, Hq, Hkv, seq_kv, D):
     return SH.decode_splits(SH.AttentionShape(batch, 1, seq_kv, Hq, Hkv, D), cus)
 
 
+def paged_plan(lengths, Hq, Hkv):
+    """(splits, slot_waves) the paged backend plans for these host-side lengths on this device."""
+    from sca_amd import host as SH
+    return SH.paged_decode_plan(lengths, Hq, Hkv, H.device_probe(0).cu_count)
+
+
 def prewarm(launch, seconds):
     """Untimed launches for `seconds`: the device's clocks ramp up under sustained load, so each
     timed leg starts from the operating point a busy device runs at."""
@@ -188,7 +194,7 @@ def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=None, 
 
 # ---- C5: paged decode ------------------------------------------------------------------------------
 def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=512, hi=16384,
-                prewarm_s=0.0):
+                prewarm_s=0.0, slot_waves=None):
     rng = np.random.default_rng(5005)
     lengths = rng.integers(lo, hi + 1, size=num_seqs).astype(np.int64)
     final = lengths + steps
@@ -196,8 +202,12 @@ def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=
     num_blocks = int(need.sum()) + 64
     perm = rng.permutation(num_blocks).astype(np.int32)
     max_blocks = int(need.max())
-    if splits is None:  # the paged path sizes splits from the pool, as the host layer does
-        splits = dispatcher_splits(num_seqs, Hq, Hkv, num_blocks * bs, D)
+    if splits is None or slot_waves is None:
+        # The paged backend's length-aware plan over the starting lengths (the cache's host
+        # lengths when the host layer attends its own page table).
+        plan_splits, plan_waves = paged_plan(lengths, Hq, Hkv)
+        splits = plan_splits if splits is None else splits
+        slot_waves = plan_waves if slot_waves is None else slot_waves
     table = np.full((num_seqs, max_blocks), -1, np.int32)
     pos = 0
     for s in range(num_seqs):
@@ -230,6 +240,7 @@ def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=
     p.dtype = H.DTYPE_BF16
     p.page_table, p.block_size, p.max_blocks_per_seq = dt.ptr, bs, max_blocks
     p.num_kv_blocks = num_blocks
+    p.slot_waves = slot_waves
     dorder = H.DeviceBuffer(num_seqs * 8)
     p.batch_order = dorder.ptr
     L = sca_amd.hip_lib()
@@ -267,7 +278,7 @@ def bench_paged(steps, num_seqs=64, bs=16, Hq=32, Hkv=8, D=128, splits=None, lo=
     ms = total_ms / steps
     nbytes = total_bytes / steps
     return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9, "splits": splits,
-            "num_blocks": num_blocks, "pool_bytes": 2 * num_blocks * bs * row_elems * 2,
+            "slot_waves": slot_waves, "num_blocks": num_blocks, "pool_bytes": 2 * num_blocks * bs * row_elems * 2,
             "mean_len": float(lengths.mean())}
 
 
@@ -397,7 +408,8 @@ def bench_paged_host(steps):
 # ---- copy calibration ------------------------------------------------------------------------------
 def bench_page_probe(steps, warmup, num_seqs=64, bs=16, Hkv=8, D=128, lo=512, hi=16384):
     """The paged decode's read pattern alone (lib/libsca_calib.so): C5's starting pool (same
-    seed, lengths, permuted page table and split count as the paged leg), K and V head slices
+    seed, lengths and permuted page table as the paged leg; the pool-sized split count of the
+    one-wave-per-slot kernel), K and V head slices
     of every page read once, nothing computed. Reported per in-flight depth (32-token tiles per
     wave, 16 KB each); the best is the practical ceiling for the paged decode kernel. Sequences
     run longest first, as the decode kernel runs a ragged batch."""
@@ -647,6 +659,7 @@ def main():
         line["paged_decode"] = {
             "value": round(pg["gbps"], 1), "unit": "GB/s", "dtype": "bf16",
             "ms_per_step": round(pg["ms"], 4), "steps": args.paged_steps,
+            "splits": pg["splits"], "slot_waves": pg["slot_waves"],
             "workload": "C5 paged decode bf16, 64 seqs L~U[512,16384], bs=16, Hq=32, Hkv=8, "
                         "D=128, permuted block table, append 1 token/seq per step",
             "roofline": {"bound": "hbm", "achieved": round(pg["gbps"], 1), "peak": PEAK_HBM_GBPS,

@@ -118,6 +118,14 @@ SCA_CAPI int sca_select(const ScaConfig* cfg, const ScaShape* shape, int32_t* ba
 SCA_CAPI void sca_explain(const ScaConfig* cfg, const ScaShape* shape, char* out, size_t len);
 SCA_CAPI void sca_recommend_tile(const ScaConfig* cfg, const ScaShape* shape, int32_t* tile4);
 SCA_CAPI int64_t sca_decode_splits(const ScaShape* shape, int64_t cu_count);
+/* Length-aware work split of the paged MFMA decode kernel (no reference counterpart: the
+ * reference sizes paged splits from the pool alone). lengths = the batch's host-side key counts;
+ * writes the split count and the sca_decode_params.slot_waves value (1 or 4; 0 with splits 1
+ * when every length is 0) the paged backend uses when the cache's own page table is attended.
+ * Returns 0, or SCA_E_SHAPE_MISMATCH. */
+SCA_CAPI int sca_paged_decode_plan(const int64_t* lengths, int64_t batch, int64_t num_heads,
+                                   int64_t num_kv_heads, int64_t cu_count, int64_t* splits,
+                                   int32_t* slot_waves);
 
 /* ---- KV helpers (kv_cache.hpp:97-110) ---- */
 SCA_CAPI int sca_compute_slot_mapping(const int32_t* row, int64_t seq_start, int64_t num_tokens,

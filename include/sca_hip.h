@@ -229,6 +229,13 @@ typedef struct sca_decode_params {
      * larger ones (up to 8192) through this scratch (no reference counterpart: the reference
      * launches sequences in batch order). NULL = batch order above 256 sequences. */
     int32_t* batch_order;
+    /* MFMA kernel work split for fp16/bf16 with head_dim 64 or 128 (no reference counterpart):
+     * 0 = library default (one wave per KV-head slot for paged KV, four for contiguous),
+     * 1 = one wave per slot (a workgroup serves four slots), 4 = four waves per slot (a
+     * workgroup serves one slot and its waves share the key tiles). Other values are rejected.
+     * Results agree either way to FP32 rounding of the merge; a planner picks the faster one
+     * per batch (sca_paged_decode_plan). */
+    int32_t slot_waves;
 } sca_decode_params;
 
 /* FP32 scratch elements the partials need: batch*num_heads*num_splits*(2 + head_dim). */

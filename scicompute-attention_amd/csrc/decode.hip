@@ -921,18 +921,20 @@ bool MfmaDecodeEnabled() {
 #endif
 }
 
-// Head slot per wave for paged KV, four waves per slot for contiguous KV. A measurement build
-// reads SCA_DECODE_WAVE_HEADS=1/0 to force either.
-bool MfmaWaveHeads(bool paged) {
+// One wave per head slot (true) or four waves per slot (false): the caller's slot_waves when
+// set, else one wave per slot for paged KV and four for contiguous KV. A measurement build reads
+// SCA_DECODE_WAVE_HEADS=1/0 to force either over both.
+bool MfmaWaveHeads(bool paged, int32_t slot_waves) {
 #ifdef SCA_MEASUREMENT_BUILD
     static const int mode = [] {
         const char* v = std::getenv("SCA_DECODE_WAVE_HEADS");
         return v == nullptr ? -1 : (v[0] == '0' ? 0 : 1);
     }();
-    return mode < 0 ? paged : mode == 1;
-#else
-    return paged;
+    if (mode >= 0) return mode == 1;
 #endif
+    if (slot_waves == 1) return true;
+    if (slot_waves == kDecodeWaves) return false;
+    return paged;
 }
 
 template <typename E, int D, bool kPaged>
@@ -961,7 +963,7 @@ int LaunchForDim(const sca_decode_params& p, hipStream_t s) {
             }
             const int h_chunks = static_cast<int>((group + kMfmaHeads - 1) / kMfmaHeads);
             const int64_t slots = p.num_kv_heads * h_chunks;
-            if (MfmaWaveHeads(kPaged)) {
+            if (MfmaWaveHeads(kPaged, p.slot_waves)) {
                 const dim3 grid(static_cast<unsigned>(p.num_splits),
                                 static_cast<unsigned>((slots + kDecodeWaves - 1) / kDecodeWaves),
                                 static_cast<unsigned>(p.batch));
@@ -1046,6 +1048,10 @@ int ValidateDecode(const sca_decode_params* p, bool paged) {
         p->v_sb % ve || p->v_sh % ve || p->v_ss % ve || p->o_sb % ve || p->o_sh % ve) {
         return SetError(SCA_E_LAYOUT_MISMATCH,
                         "decode: pointers must be 16 B aligned and strides multiples of 16 B");
+    }
+    if (p->slot_waves != 0 && p->slot_waves != 1 && p->slot_waves != kDecodeWaves) {
+        return SetError(SCA_E_SHAPE_MISMATCH, "decode: slot_waves must be 0, 1 or 4; got " +
+                                                  std::to_string(p->slot_waves));
     }
     if ((reinterpret_cast<uintptr_t>(p->batch_order) & 7u) != 0) {
         return SetError(SCA_E_LAYOUT_MISMATCH, "decode: batch_order must be 8 B aligned");

@@ -88,6 +88,7 @@ class DecodeParams(ctypes.Structure):
         ("scale", ctypes.c_float), ("dtype", c_i32),
         ("page_table", c_vp), ("block_size", c_i64), ("max_blocks_per_seq", c_i64),
         ("num_kv_blocks", c_i64), ("seq_lens", c_vp), ("batch_order", c_vp),
+        ("slot_waves", c_i32),
     ]
 
 

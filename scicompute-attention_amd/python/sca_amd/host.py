@@ -98,6 +98,8 @@ _SIGS = [
                            ctypes.c_size_t]),
     ("sca_recommend_tile", None, [ctypes.POINTER(ScaConfig), ctypes.POINTER(ScaShape), c_i32 * 4]),
     ("sca_decode_splits", c_i64, [ctypes.POINTER(ScaShape), c_i64]),
+    ("sca_paged_decode_plan", ctypes.c_int, [c_vp, c_i64, c_i64, c_i64, c_i64,
+                                              ctypes.POINTER(c_i64), ctypes.POINTER(c_i32)]),
     ("sca_compute_slot_mapping", ctypes.c_int, [c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
     ("sca_kv_cache_bytes", ctypes.c_int, [ctypes.POINTER(ScaKvConfig), ctypes.POINTER(c_u64)]),
     ("sca_max_blocks_for_budget", c_i64, [ctypes.POINTER(ScaKvConfig), c_u64]),
@@ -446,6 +448,17 @@ def explain(cfg: AttentionConfig, shape: AttentionShape) -> str:
 def decode_splits(shape: AttentionShape, cu_count: int) -> int:
     s = shape.to_c()
     return host_lib().sca_decode_splits(ctypes.byref(s), cu_count)
+
+
+def paged_decode_plan(lengths, num_heads: int, num_kv_heads: int, cu_count: int):
+    """(splits, slot_waves) of the paged MFMA decode kernel for a batch of host-side lengths:
+    the plan the paged backend applies when it attends the cache's own page table."""
+    lens = np.ascontiguousarray(lengths, dtype=np.int64)
+    splits, waves = c_i64(0), c_i32(0)
+    _raise(host_lib().sca_paged_decode_plan(_ptr(lens) if lens.size else None, lens.size,
+                                            num_heads, num_kv_heads, cu_count,
+                                            ctypes.byref(splits), ctypes.byref(waves)))
+    return int(splits.value), int(waves.value)
 
 
 def compute_slot_mapping(row, seq_start, num_tokens, block_size, max_blocks):

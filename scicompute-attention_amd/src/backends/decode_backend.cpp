@@ -5,6 +5,7 @@
 // the split count comes from the MI355X dispatch table (runtime/dispatch_table.hpp).
 
 #include <string>
+#include <vector>
 
 #include "runtime/dispatch_table.hpp"
 #include "runtime/internal.hpp"
@@ -313,8 +314,26 @@ sci::Result<AttentionResult> RunPaged(const sci::Tensor& q, const PagedKVCache& 
         params.max_blocks_per_seq > 0 ? params.max_blocks_per_seq : kv.MaxBlocksPerSeq();
     // Upper bound of a sequence's length; the kernel reads the true lengths from seq_lens.
     const int64_t seq_kv_bound = kv_cfg.num_blocks * block_size;
-    const int64_t splits =
+    int64_t splits =
         ResolveSplits(cfg.num_splits, num_seqs, num_heads, kv_cfg.num_kv_heads, seq_kv_bound);
+    int32_t slot_waves = 0;
+    // With the cache's own page table, its host-side lengths say how ragged the batch is; the
+    // MFMA kernel (fp16/bf16, head_dim 64 or 128, power-of-two pages) then takes the split count
+    // and slot work split of the length-aware plan.
+    const bool mfma_shape = kv_cfg.dtype != sci::DType::kFloat32 &&
+                            (head_dim == 64 || head_dim == 128) &&
+                            (block_size & (block_size - 1)) == 0;
+    if (cfg.num_splits <= 0 && params.page_table == nullptr && mfma_shape) {
+        std::vector<int64_t> lengths(static_cast<size_t>(num_seqs));
+        for (int64_t b = 0; b < num_seqs; ++b) lengths[static_cast<size_t>(b)] = kv.SeqLength(b);
+        const auto plan = detail::PagedDecodePlan(lengths.data(), num_seqs, num_heads,
+                                                  kv_cfg.num_kv_heads,
+                                                  DeviceCapability::ForDevice(0).sm_count);
+        if (plan.slot_waves != 0) {
+            splits = plan.splits;
+            slot_waves = plan.slot_waves;
+        }
+    }
 
     AttentionResult result;
     result.out = sci::Tensor(sci::TensorShape({num_seqs, num_heads, seq_q, head_dim}), q.dtype(),
@@ -346,6 +365,7 @@ sci::Result<AttentionResult> RunPaged(const sci::Tensor& q, const PagedKVCache& 
     p.max_blocks_per_seq = max_blocks;
     p.num_kv_blocks = kv_cfg.num_blocks;
     p.seq_lens = params.seq_lens;
+    p.slot_waves = slot_waves;
     size_t partial_bytes = 0;
     sci::Status status = BindPartials(&p, splits, q.device().id(), &partial_bytes);
     if (status.ok()) {
@@ -357,7 +377,8 @@ sci::Result<AttentionResult> RunPaged(const sci::Tensor& q, const PagedKVCache& 
     result.stats.workspace_bytes = partial_bytes;
     result.stats.num_splits = splits;
     result.stats.kv_bytes = kv.Storage().MemoryBytes();
-    result.stats.note = "paged decode: " + std::to_string(splits) + " splits, block_size=" +
+    result.stats.note = "paged decode: " + std::to_string(splits) + " splits, " +
+                        (slot_waves == 4 ? "four waves" : "one wave") + " per head slot, block_size=" +
                         std::to_string(block_size) + ", layer=" + std::to_string(params.layer);
     return sci::Ok(std::move(result));
 }

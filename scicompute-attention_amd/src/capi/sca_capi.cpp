@@ -227,6 +227,20 @@ void sca_recommend_tile(const ScaConfig* cfg, const ScaShape* shape, int32_t* ti
 int64_t sca_decode_splits(const ScaShape* s, int64_t cu_count) {
     return sca::detail::DecodeSplits(s->batch, s->num_heads, s->num_kv_heads, s->seq_kv, cu_count);
 }
+int sca_paged_decode_plan(const int64_t* lengths, int64_t batch, int64_t num_heads,
+                          int64_t num_kv_heads, int64_t cu_count, int64_t* splits,
+                          int32_t* slot_waves) {
+    if (lengths == nullptr || splits == nullptr || slot_waves == nullptr || batch < 1 ||
+        num_kv_heads < 1 || num_heads < num_kv_heads || num_heads % num_kv_heads != 0) {
+        return Fail(sca::MakeStatus(sca::AttnStatusCode::kShapeMismatch,
+                                    "sca_paged_decode_plan: null pointer or invalid heads/batch"));
+    }
+    const auto plan =
+        sca::detail::PagedDecodePlan(lengths, batch, num_heads, num_kv_heads, cu_count);
+    *splits = plan.splits;
+    *slot_waves = plan.slot_waves;
+    return 0;
+}
 
 int sca_compute_slot_mapping(const int32_t* row, int64_t seq_start, int64_t num_tokens,
                              int64_t block_size, int64_t max_blocks, int32_t* slots) {

@@ -276,6 +276,11 @@ def test_serving_loop_paged_decode(hip, dtype):
                                 {"seq_lens": dl.data_ptr, "num_seqs": seqs, "block_size": bs},
                                 H.AttentionConfig())
         assert res.stats["used_backend"] == H.BACKENDS["paged"]
+        # the cache's host lengths drive the length-aware plan (a ragged batch of six sequences
+        # gets four waves per KV-head slot)
+        splits, waves = H.paged_decode_plan(lens, Hq, Hkv, H.host_lib().sca_device_cu_count())
+        assert waves == 4 and res.stats["num_splits"] == splits, res.stats
+        assert "four waves per head slot" in res.stats["note"], res.stats["note"]
         out = out_float(res, dtype)
         for s in range(seqs):
             ref, _ = orc.reference_attention(qd[s:s + 1], srv.k[s].transpose(1, 0, 2)[None],

@@ -40,7 +40,7 @@ def build_pool(lengths, bs, Hkv, D, dtype, seed, slack=3, gen="uniform"):
 
 
 def run_paged(qb, kb, vb, table, lengths, dtype, *, Hq, Hkv, D, bs, num_blocks, splits,
-              pass_lens=True, longest_first=True):
+              pass_lens=True, longest_first=True, slot_waves=0):
     S = len(lengths)
     max_blocks = table.shape[1]
     dq = H.DeviceBuffer.from_array(qb)
@@ -59,6 +59,7 @@ def run_paged(qb, kb, vb, table, lengths, dtype, *, Hq, Hkv, D, bs, num_blocks, 
     p.seq_lens = dl.ptr if pass_lens else None
     order = H.DeviceBuffer(8 * S)
     p.batch_order = order.ptr if longest_first else None
+    p.slot_waves = slot_waves
     H.decode_splitk_paged(p)
     sca_amd.synchronize()
     return to_float(dout.download(np.uint16), dtype).reshape(S, Hq, D)
@@ -75,23 +76,27 @@ def reference(qd, kd, vd, table, lengths, bs, num_blocks):
     return np.concatenate(outs)
 
 
-def _case(lengths, bs, Hq, Hkv, D, dtype, seed, splits=16, gen="uniform", longest_first=True):
+def _case(lengths, bs, Hq, Hkv, D, dtype, seed, splits=16, gen="uniform", longest_first=True,
+          slot_waves=0):
     nb, mb, table, kb, kd, vb, vd = build_pool(lengths, bs, Hkv, D, dtype, seed, gen=gen)
     q = uniform((len(lengths), Hq, 1, D), seed) if gen == "uniform" else \
         normal((len(lengths), Hq, 1, D), seed)
     qb, qd = quantize(q, dtype)
     out = run_paged(qb, kb, vb, table, lengths, dtype, Hq=Hq, Hkv=Hkv, D=D, bs=bs, num_blocks=nb,
-                    splits=splits, longest_first=longest_first)
+                    splits=splits, longest_first=longest_first, slot_waves=slot_waves)
     ref = reference(qd, kd, vd, table, lengths, bs, nb)
     tag = (f"paged {dtype} lens={lengths[:4]} bs={bs} Hq={Hq} Hkv={Hkv} D={D} splits={splits} "
-           f"longest_first={longest_first}")
+           f"longest_first={longest_first} slot_waves={slot_waves}")
     print(tag, flush=True)
     check_attention(out.reshape(-1, D), ref, dtype, tag)
 
 
+# slot_waves: 0 = the paged default (one wave per KV-head slot), 4 = four waves share a slot's
+# key tiles (the plan's choice for ragged batches with few slots per CU).
+@pytest.mark.parametrize("slot_waves", [0, 4])
 @pytest.mark.parametrize("bs", [1, 8, 16, 32])
-def test_every_block_size(hip, bs):
-    _case([257], bs, 8, 8, 128, "f16", 80000 + bs)
+def test_every_block_size(hip, bs, slot_waves):
+    _case([257], bs, 8, 8, 128, "f16", 80000 + bs, slot_waves=slot_waves)
 
 
 @pytest.mark.parametrize("group", [1, 2, 4])
@@ -107,6 +112,20 @@ def test_many_ragged_sequences_bf16(hip):
     _case(lengths, 16, 32, 8, 128, "bf16", 82002, splits=1, gen="normal")
     _case(lengths, 16, 32, 8, 128, "bf16", 82003, splits=3, gen="normal", longest_first=False)
     _case(lengths + [0, 5], 16, 32, 8, 64, "f16", 82004, splits=4)
+    _case(lengths, 16, 32, 8, 128, "bf16", 82005, splits=6, gen="normal", slot_waves=4)
+    _case(lengths + [0, 5], 16, 32, 8, 64, "f16", 82006, splits=3, slot_waves=4,
+          longest_first=False)
+    _case(lengths, 16, 64, 4, 128, "bf16", 82007, splits=2, gen="normal", slot_waves=1)
+
+
+def test_slot_waves_outside_0_1_4_rejected(hip):
+    lengths = [40]
+    nb, mb, table, kb, kd, vb, vd = build_pool(lengths, 16, 2, 64, "f16", 82101)
+    qb, _ = quantize(uniform((1, 8, 1, 64), 82101), "f16")
+    for bad in (2, 3, 8, -1):
+        with pytest.raises(H.HipError, match="slot_waves"):
+            run_paged(qb, kb, vb, table, lengths, "f16", Hq=8, Hkv=2, D=64, bs=16, num_blocks=nb,
+                      splits=2, slot_waves=bad)
 
 
 def test_unmapped_pages_contribute_nothing(hip):
@@ -158,11 +177,12 @@ def test_nan_outside_attended_rows_is_never_used(hip, bs, D):
     vb[~used] = 0x7FC0
     q = uniform((len(lengths), Hq, 1, D), 85001)
     qb, qd = quantize(q, "bf16")
-    for splits in (1, 3):
+    ref = reference(qd, kd, vd, table, lengths, bs, nb)
+    for splits, waves in ((1, 0), (3, 0), (1, 4), (3, 4)):
         out = run_paged(qb, kb, vb, table, lengths, "bf16", Hq=Hq, Hkv=Hkv, D=D, bs=bs,
-                        num_blocks=nb, splits=splits)
-        ref = reference(qd, kd, vd, table, lengths, bs, nb)
-        check_attention(out.reshape(-1, D), ref, "bf16", f"paged NaN pool bs={bs} D={D}")
+                        num_blocks=nb, splits=splits, slot_waves=waves)
+        check_attention(out.reshape(-1, D), ref, "bf16",
+                        f"paged NaN pool bs={bs} D={D} splits={splits} slot_waves={waves}")
 
 
 def test_large_ragged_batch_ranked_through_scratch(hip):
@@ -171,6 +191,7 @@ def test_large_ragged_batch_ranked_through_scratch(hip):
     lengths = rng.integers(0, 90, size=300).tolist()
     _case(lengths, 16, 8, 2, 64, "f16", 86001, splits=2)
     _case(lengths, 16, 8, 2, 64, "f16", 86002, splits=3, longest_first=False)
+    _case(lengths, 16, 8, 2, 64, "f16", 86003, splits=2, slot_waves=4)
 
 
 
@@ -186,7 +207,9 @@ def _bf16_to_f32(bits):
 
 def test_c5_full_size_against_fp32(hip):
     """C5 at its full shape (64 sequences, L ~ U[512, 16384], bs 16, Hq 32, Hkv 8, D 128, bf16,
-    12 splits as the dispatcher picks them, permuted block table, 2.2 GB pool). Each sequence
+    permuted block table, 2.2 GB pool), run twice: 12 splits with one wave per KV-head slot (the
+    pool-sized split count) and 3 splits with four waves per slot (the length-aware plan on a
+    256-CU MI355X). Each sequence
     is checked against an fp32 softmax(q k^T * scale) v over the rows its block table gathers
     (page_table.cuh:18-36), within the bf16 tolerance of the other paged cases (max abs error
     <= 1.6e-2 of max |ref|)."""
@@ -204,9 +227,13 @@ def test_c5_full_size_against_fp32(hip):
     kb = _bf16_normal(rng, (nb * bs, Hkv, D))
     vb = _bf16_normal(rng, (nb * bs, Hkv, D))
     qb = _bf16_normal(rng, (S, Hq, 1, D))
-    print(f"paged C5 full size: seqs={S} pool blocks={nb} splits={splits}", flush=True)
-    got = run_paged(qb, kb, vb, table, lengths.tolist(), "bf16", Hq=Hq, Hkv=Hkv, D=D, bs=bs,
-                    num_blocks=nb, splits=splits)
+    runs = {}
+    for sp, waves in ((splits, 1), (3, 4)):
+        print(f"paged C5 full size: seqs={S} pool blocks={nb} splits={sp} slot_waves={waves}",
+              flush=True)
+        runs[(sp, waves)] = run_paged(qb, kb, vb, table, lengths.tolist(), "bf16", Hq=Hq,
+                                      Hkv=Hkv, D=D, bs=bs, num_blocks=nb, splits=sp,
+                                      slot_waves=waves)
 
     scale = np.float32(1.0 / np.sqrt(D))
     qf = _bf16_to_f32(qb).reshape(S, Hkv, Hq // Hkv, D)  # query heads grouped by KV head
@@ -221,15 +248,20 @@ def test_c5_full_size_against_fp32(hip):
         w = np.exp(sc)
         w /= w.sum(axis=-1, keepdims=True)
         ref[s] = np.matmul(w, vs).reshape(Hq, D)
-    check_attention(got.reshape(-1, D), ref.reshape(-1, D), "bf16", "paged C5 full size")
+    for (sp, waves), got in runs.items():
+        check_attention(got.reshape(-1, D), ref.reshape(-1, D), "bf16",
+                        f"paged C5 full size splits={sp} slot_waves={waves}")
 
 
 @pytest.mark.parametrize("bs,L,splits", [(2, 9001, 2), (2, 9001, 3), (1, 5000, 1), (4, 20001, 2),
                                          (16, 40000, 1)])
-@pytest.mark.parametrize("D,dtype", [(128, "bf16"), (96, "f16")])
-def test_splits_spanning_several_page_segments(hip, bs, L, splits, D, dtype):
+@pytest.mark.parametrize("D,dtype,slot_waves", [(128, "bf16", 0), (128, "bf16", 4),
+                                                (96, "f16", 0)])
+def test_splits_spanning_several_page_segments(hip, bs, L, splits, D, dtype, slot_waves):
     """Splits longer than one staged page-id segment (2048 pages), starting on and off a page
     boundary: the segment loop restages the page ids of every segment. D=128 bf16 runs the MFMA
-    kernel, D=96 the VALU kernel."""
-    print(f"paged multi-segment bs={bs} L={L} splits={splits} D={D} {dtype}", flush=True)
-    _case([L, 3], bs, 8, 2, D, dtype, 87000 + bs + splits + D, splits=splits)
+    kernel (one or four waves per KV-head slot), D=96 the VALU kernel."""
+    print(f"paged multi-segment bs={bs} L={L} splits={splits} D={D} {dtype} "
+          f"slot_waves={slot_waves}", flush=True)
+    _case([L, 3], bs, 8, 2, D, dtype, 87000 + bs + splits + D, splits=splits,
+          slot_waves=slot_waves)
