@@ -166,7 +166,8 @@ def bench_flash_gqa(steps, warmup, B=4, Hq=32, Hkv=8, S=8192, D=128, prewarm_s=0
 
 
 # ---- C4: split-K decode --------------------------------------------------------------------------
-def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=None, prewarm_s=0.0):
+def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=None, prewarm_s=0.0,
+                 slot_waves=0):
     if splits is None:
         splits = dispatcher_splits(B, Hq, Hkv, S, D)
     rng = np.random.default_rng(4004)
@@ -186,6 +187,7 @@ def bench_decode(steps, warmup, B=16, Hq=32, Hkv=8, S=4096, D=128, splits=None, 
     p.o_sb, p.o_sh = Hq * D, D
     p.scale = float(np.float32(1.0 / np.sqrt(D)))
     p.dtype = H.DTYPE_F16
+    p.slot_waves = slot_waves
     prewarm(lambda: H.decode_splitk(p), prewarm_s)
     ms = time_launches(lambda: H.decode_splitk(p), steps, warmup)
     nbytes = 2 * B * Hkv * S * D * 2 + 2 * B * Hq * D * 2
@@ -408,8 +410,7 @@ def bench_paged_host(steps):
 # ---- copy calibration ------------------------------------------------------------------------------
 def bench_page_probe(steps, warmup, num_seqs=64, bs=16, Hkv=8, D=128, lo=512, hi=16384):
     """The paged decode's read pattern alone (lib/libsca_calib.so): C5's starting pool (same
-    seed, lengths and permuted page table as the paged leg; the pool-sized split count of the
-    one-wave-per-slot kernel), K and V head slices
+    seed, lengths and permuted page table as the paged leg; 12 splits), K and V head slices
     of every page read once, nothing computed. Reported per in-flight depth (32-token tiles per
     wave, 16 KB each); the best is the practical ceiling for the paged decode kernel. Sequences
     run longest first, as the decode kernel runs a ragged batch."""
@@ -425,7 +426,7 @@ def bench_page_probe(steps, warmup, num_seqs=64, bs=16, Hkv=8, D=128, lo=512, hi
     for s in range(num_seqs):
         table[s, : need[s]] = perm[pos: pos + need[s]]
         pos += need[s]
-    splits = dispatcher_splits(num_seqs, 32, Hkv, num_blocks * bs, D)
+    splits = 12  # the one-wave-per-slot kernel's pool-sized split count for C5 on 256 CUs
     # Longest sequences first, as the decode kernel schedules a ragged batch.
     order = np.argsort(-lengths, kind="stable")
     table, lengths = np.ascontiguousarray(table[order]), lengths[order]

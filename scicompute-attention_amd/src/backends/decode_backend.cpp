@@ -26,11 +26,11 @@ int64_t PartialElements(int64_t batch, int64_t heads, int64_t splits, int64_t he
 
 // Explicit split counts are honoured up to the table's cap; otherwise the table decides.
 int64_t ResolveSplits(int64_t requested, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
-                      int64_t seq_kv) {
+                      int64_t seq_kv, int slot_waves = 4) {
     const auto& th = detail::kDispatchThresholds;
     if (requested > 0) return requested < th.max_splits ? requested : th.max_splits;
     return detail::DecodeSplits(batch, num_heads, num_kv_heads, seq_kv,
-                                DeviceCapability::ForDevice(0).sm_count);
+                                DeviceCapability::ForDevice(0).sm_count, slot_waves);
 }
 
 // Points the partial pointers of `p` into the pooled FP32 scratch (m | l | O).
@@ -217,7 +217,7 @@ public:
 
     size_t WorkspaceBytes(const AttentionConfig& cfg, const AttentionShape& shape) const override {
         const int64_t splits = ResolveSplits(cfg.num_splits, shape.batch, shape.num_heads,
-                                             shape.num_kv_heads, shape.seq_kv);
+                                             shape.num_kv_heads, shape.seq_kv, /*slot_waves=*/1);
         if (splits <= 1) return 0;
         return static_cast<size_t>(
                    PartialElements(shape.batch, shape.num_heads, splits, shape.head_dim)) *
@@ -315,7 +315,8 @@ sci::Result<AttentionResult> RunPaged(const sci::Tensor& q, const PagedKVCache& 
     // Upper bound of a sequence's length; the kernel reads the true lengths from seq_lens.
     const int64_t seq_kv_bound = kv_cfg.num_blocks * block_size;
     int64_t splits =
-        ResolveSplits(cfg.num_splits, num_seqs, num_heads, kv_cfg.num_kv_heads, seq_kv_bound);
+        ResolveSplits(cfg.num_splits, num_seqs, num_heads, kv_cfg.num_kv_heads, seq_kv_bound,
+                      /*slot_waves=*/1);
     int32_t slot_waves = 0;
     // With the cache's own page table, its host-side lengths say how ragged the batch is; the
     // MFMA kernel (fp16/bf16, head_dim 64 or 128, power-of-two pages) then takes the split count

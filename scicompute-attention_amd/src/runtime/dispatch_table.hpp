@@ -32,19 +32,32 @@ inline constexpr DispatchThresholds kDispatchThresholds{
     /* revision             */ "r0-mi355x",
 };
 
-// Split count of the decode kernels for `batch` sequences of up to `seq_kv` keys. The MFMA
-// kernel runs one workgroup per (sequence, split, four KV-head slots), a slot being one KV head
-// and up to 16 of its query heads; splits are added until every CU holds `workgroups_per_cu`
-// workgroups, while each split keeps at least `min_tokens_per_split` keys.
+// Split count of the decode kernels for `batch` sequences of up to `seq_kv` keys. A head slot is
+// one KV head and up to 16 of its query heads; the MFMA kernel runs a workgroup per (sequence,
+// split, slot) with four waves per slot (slot_waves = 4, the contiguous default) or per (sequence,
+// split, four slots) with one wave per slot (slot_waves = 1, the paged default).
+//  - Four waves per slot: a batch with at least one slot per CU runs unsplit, which also skips
+//    the combine kernel (measured on MI355X, fp16, H_q 32, H_kv 8, D 128: 64 x 4096 keys 6.07 TB/s
+//    against 5.65 at 8 splits; 128 x 2048 6.02 against 5.64; 32 x 4096 5.74 against 5.42);
+//    smaller batches take splits until every CU holds 4 workgroups (C4, 16 x 4096: 8 splits,
+//    5.97 TB/s; 8 x 32768: 16 splits, 5.77 against 5.47 at 64).
+//  - One wave per slot: splits are added until every CU holds `workgroups_per_cu` workgroups.
+// Each split keeps at least `min_tokens_per_split` keys.
 inline int64_t DecodeSplits(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
-                            int64_t seq_kv, int64_t cu_count) {
+                            int64_t seq_kv, int64_t cu_count, int slot_waves = 4) {
     const auto& th = kDispatchThresholds;
     if (batch < 1 || num_kv_heads < 1 || seq_kv < 1) return 1;
     const int64_t group = num_heads / num_kv_heads;
     const int64_t slots = num_kv_heads * ((group + 15) / 16);
-    const int64_t wgs_per_split = batch * ((slots + 3) / 4);
     const int64_t cus = cu_count > 0 ? cu_count : 256;
-    int64_t splits = (th.workgroups_per_cu * cus + wgs_per_split - 1) / wgs_per_split;
+    int64_t splits;
+    if (slot_waves == 1) {
+        const int64_t wgs_per_split = batch * ((slots + 3) / 4);
+        splits = (th.workgroups_per_cu * cus + wgs_per_split - 1) / wgs_per_split;
+    } else {
+        const int64_t jobs = batch * slots;
+        splits = jobs >= cus ? 1 : (4 * cus + jobs - 1) / jobs;
+    }
     const int64_t by_length = (seq_kv + th.min_tokens_per_split - 1) / th.min_tokens_per_split;
     if (splits > by_length) splits = by_length;
     if (splits > th.max_splits) splits = th.max_splits;

@@ -72,3 +72,15 @@ def test_plan_rejects_invalid_heads():
         H.paged_decode_plan([10], 6, 4, CUS)
     with pytest.raises(Exception):
         H.paged_decode_plan([], 32, 8, CUS)
+
+
+@pytest.mark.parametrize("B,S,want", [
+    (16, 4096, 8),    # C4: 128 slots -> four workgroups per CU (5.97 TB/s)
+    (64, 4096, 1),    # a slot per CU or more runs unsplit, no combine (6.07 TB/s vs 5.65 at 8)
+    (128, 2048, 1),   # (6.02 vs 5.64 at 4)
+    (32, 4096, 1),    # (5.74 vs 5.42 at 8)
+    (8, 32768, 16),   # (5.77 vs 5.47 at 64)
+    (1, 2048, 4),     # each split keeps 512 keys
+])
+def test_contiguous_decode_splits(B, S, want):
+    assert H.decode_splits(H.AttentionShape(B, 1, S, 32, 8, 128), CUS) == want
