@@ -39,8 +39,10 @@ inline constexpr DispatchThresholds kDispatchThresholds{
 //  - Four waves per slot: a batch with at least one slot per CU runs unsplit, which also skips
 //    the combine kernel (measured on MI355X, fp16, H_q 32, H_kv 8, D 128: 64 x 4096 keys 6.07 TB/s
 //    against 5.65 at 8 splits; 128 x 2048 6.02 against 5.64; 32 x 4096 5.74 against 5.42);
-//    smaller batches take splits until every CU holds 4 workgroups (C4, 16 x 4096: 8 splits,
-//    5.97 TB/s; 8 x 32768: 16 splits, 5.77 against 5.47 at 64).
+//    smaller batches take splits until every CU holds 4 workgroups, but no more than 8 unless
+//    fewer would leave CUs without a workgroup (C4, 16 x 4096: 8 splits, 5.97 TB/s; 8 x 32768:
+//    8 splits, 5.95 against 5.47 at 64; 4 x 16384: 8, 5.84 against 5.66 at 32; 1 x 65536: 32,
+//    5.60 against 5.22 at 64).
 //  - One wave per slot: splits are added until every CU holds `workgroups_per_cu` workgroups.
 // Each split keeps at least `min_tokens_per_split` keys.
 inline int64_t DecodeSplits(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
@@ -56,7 +58,13 @@ inline int64_t DecodeSplits(int64_t batch, int64_t num_heads, int64_t num_kv_hea
         splits = (th.workgroups_per_cu * cus + wgs_per_split - 1) / wgs_per_split;
     } else {
         const int64_t jobs = batch * slots;
-        splits = jobs >= cus ? 1 : (4 * cus + jobs - 1) / jobs;
+        if (jobs >= cus) {
+            splits = 1;
+        } else {
+            const int64_t fill = (cus + jobs - 1) / jobs;  // one workgroup per CU
+            const int64_t four = (4 * cus + jobs - 1) / jobs;
+            splits = four < 8 ? four : (fill > 8 ? fill : 8);
+        }
     }
     const int64_t by_length = (seq_kv + th.min_tokens_per_split - 1) / th.min_tokens_per_split;
     if (splits > by_length) splits = by_length;

@@ -79,7 +79,10 @@ def test_plan_rejects_invalid_heads():
     (64, 4096, 1),    # a slot per CU or more runs unsplit, no combine (6.07 TB/s vs 5.65 at 8)
     (128, 2048, 1),   # (6.02 vs 5.64 at 4)
     (32, 4096, 1),    # (5.74 vs 5.42 at 8)
-    (8, 32768, 16),   # (5.77 vs 5.47 at 64)
+    (8, 32768, 8),    # at most 8 splits (5.95 vs 5.47 at 64)
+    (4, 16384, 8),    # (5.84 vs 5.66 at 32)
+    (1, 65536, 32),   # unless fewer leave CUs idle (5.60 vs 5.22 at 64)
+    (24, 4096, 6),    # four workgroups per CU
     (1, 2048, 4),     # each split keeps 512 keys
 ])
 def test_contiguous_decode_splits(B, S, want):
