@@ -133,8 +133,9 @@ def decode_params(dq, dk, dv, dout, parts, *, B, Hq, Hkv, Skv, D, splits, dtype,
     return p
 
 
-def run_decode(qb, kb, vb, dtype, *, B, Hq, Hkv, Skv, D, splits, seq_lens=None):
-    """Contiguous split-K decode: q [B,Hq,1,D], k/v [B,Hkv,Skv,D] storage arrays."""
+def run_decode(qb, kb, vb, dtype, *, B, Hq, Hkv, Skv, D, splits, seq_lens=None, slot_waves=0):
+    """Contiguous split-K decode: q [B,Hq,1,D], k/v [B,Hkv,Skv,D] storage arrays. slot_waves:
+    0 = library default, 1 = one wave per KV-head slot, 4 = four waves per slot."""
     dq = H.DeviceBuffer.from_array(qb)
     dk = H.DeviceBuffer.from_array(kb)
     dv = H.DeviceBuffer.from_array(vb)
@@ -146,6 +147,7 @@ def run_decode(qb, kb, vb, dtype, *, B, Hq, Hkv, Skv, D, splits, seq_lens=None):
     if seq_lens is not None:
         lens_buf = H.DeviceBuffer.from_array(np.asarray(seq_lens, dtype=np.int32))
         p.seq_lens = lens_buf.ptr
+    p.slot_waves = slot_waves
     H.decode_splitk(p)
     sca_amd.synchronize()
     raw = dout.download(np.uint32 if dtype == "f32" else np.uint16)

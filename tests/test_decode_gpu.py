@@ -15,7 +15,7 @@ from attn_util import (check_attention, decode_params, normal, quantize, run_dec
 pytestmark = pytest.mark.gpu
 
 
-def _case(dtype, B, Hq, Hkv, Skv, D, splits, seed, abs_gate=True, seq_lens=None):
+def _case(dtype, B, Hq, Hkv, Skv, D, splits, seed, abs_gate=True, seq_lens=None, slot_waves=0):
     q = uniform((B, Hq, 1, D), seed)
     k = uniform((B, Hkv, Skv, D), seed + 101)
     v = uniform((B, Hkv, Skv, D), seed + 202)
@@ -23,8 +23,9 @@ def _case(dtype, B, Hq, Hkv, Skv, D, splits, seed, abs_gate=True, seq_lens=None)
     kb, kd = quantize(k, dtype) if dtype != "f32" else (k.view(np.uint32), k)
     vb, vd = quantize(v, dtype) if dtype != "f32" else (v.view(np.uint32), v)
     out = run_decode(qb, kb, vb, dtype, B=B, Hq=Hq, Hkv=Hkv, Skv=Skv, D=D, splits=splits,
-                     seq_lens=seq_lens)
-    tag = f"decode {dtype} B={B} Hq={Hq} Hkv={Hkv} Skv={Skv} D={D} splits={splits} seed={seed}"
+                     seq_lens=seq_lens, slot_waves=slot_waves)
+    tag = (f"decode {dtype} B={B} Hq={Hq} Hkv={Hkv} Skv={Skv} D={D} splits={splits} seed={seed} "
+           f"slot_waves={slot_waves}")
     print(tag, flush=True)
     if seq_lens is None:
         ref, _ = orc.reference_attention(qd, kd, vd, True)
@@ -125,3 +126,14 @@ def test_groups_wider_than_one_mfma_tile(hip):
     _case("f16", 2, 32, 1, 700, 128, 3, 77001)
     _case("bf16", 1, 24, 1, 515, 64, 2, 77002)
     _case("bf16", 2, 16, 1, 95, 128, 1, 77003)
+
+
+@pytest.mark.parametrize("slot_waves", [1, 4])
+def test_contiguous_slot_layouts(hip, slot_waves):
+    """Both MFMA work splits on contiguous KV: one wave per KV-head slot (workgroups of four
+    slots, the last one partly empty when the slot count is not a multiple of four) and four
+    waves per slot; ragged lengths, empty splits and a group wider than one MFMA tile."""
+    _case("f16", 3, 24, 6, 1500, 128, 3, 76001, slot_waves=slot_waves)
+    _case("bf16", 2, 8, 8, 700, 64, 1, 76002, slot_waves=slot_waves)
+    _case("f16", 4, 8, 2, 600, 128, 16, 76003, seq_lens=[600, 3, 1, 257], slot_waves=slot_waves)
+    _case("bf16", 1, 32, 1, 900, 128, 2, 76004, slot_waves=slot_waves)
