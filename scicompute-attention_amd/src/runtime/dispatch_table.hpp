@@ -75,10 +75,11 @@ inline int64_t DecodeSplits(int64_t batch, int64_t num_heads, int64_t num_kv_hea
 // Work split of the paged MFMA decode kernel for a batch whose host-side lengths are known.
 // slot_waves = 1: one wave per head slot, a workgroup serves four slots; 4: four waves share one
 // slot's key tiles. Measured on MI355X over 48-step decode loops (bf16, H_q 32, H_kv 8, D 128):
-//  - near-uniform batches (longest <= 5/4 of the mean) that leave some CUs free with one split:
+//  - near-uniform batches (longest <= 11/10 of the mean) that leave some CUs free with one split:
 //    one wave per slot, one workgroup per CU (uniform 64 x 8448 keys: 5.89 TB/s vs 5.58);
 //  - ragged batches with at most two slots per CU: four waves per slot, `workgroups_per_cu`
-//    workgroups per CU (C5, 64 x 512..16384: 5.74 TB/s vs 5.61; 16 sequences: 4.98 vs 4.26);
+//    workgroups per CU (C5, 64 x 512..16384: 5.74 TB/s vs 5.61; 16 sequences: 4.98 vs 4.26;
+//    64 x 6000..10000: 5.55 vs 5.41 for one wave per slot at one workgroup per CU);
 //  - otherwise (many sequences): one wave per slot, `workgroups_per_cu` workgroups per CU
 //    (256 x 512..4096: 5.56 TB/s vs 5.54).
 // Each split keeps at least `min_tokens_per_split` keys of the longest sequence.
@@ -106,7 +107,7 @@ inline PagedDecodePlanResult PagedDecodePlan(const int64_t* lengths, int64_t bat
     const int64_t slots = num_kv_heads * ((group + 15) / 16);
     const int64_t quads = (slots + 3) / 4;
     const int64_t cus = cu_count > 0 ? cu_count : 256;
-    const bool uniform = 4 * longest * batch <= 5 * total;
+    const bool uniform = 10 * longest * batch <= 11 * total;
     int64_t splits;
     int32_t slot_waves;
     if (uniform && batch * quads <= cus) {

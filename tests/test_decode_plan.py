@@ -28,6 +28,9 @@ def lengths_uniform_random(n, lo, hi, seed=5005):
     ("ragged16", lengths_uniform_random(16, 512, 16384), (12, 4)),
     # 128 ragged sequences (four slots per CU): one wave per slot, 6 splits (5.57 TB/s)
     ("ragged128", lengths_uniform_random(128, 128, 8192), (6, 1)),
+    # mildly ragged (longest 5/4 of the mean): four waves per slot, 3 splits (5.55 TB/s; one
+    # wave per slot at one workgroup per CU: 5.41)
+    ("mild64", lengths_uniform_random(64, 6000, 10000), (3, 4)),
     # 256 ragged sequences: one wave per slot, 3 splits (5.56 TB/s; four waves: 5.54 at 1)
     ("ragged256", lengths_uniform_random(256, 512, 4096), (3, 1)),
 ])
