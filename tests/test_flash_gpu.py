@@ -285,3 +285,18 @@ def test_kv_extent_beyond_2gib_falls_back(hip, causal):
     out = to_float(dout.download(np.uint16), dtype).reshape(Sq, D)
     ref, _ = orc.reference_attention(qd, kd, vd, causal)
     check_attention(out, ref, dtype, f"2 GiB extent causal={causal}", abs_gate=True)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,dtype", [
+    (2, 8, 4, 300, 128, "f16"),    # 8 (batch, KV head) groups of 2 heads: XCD order, wide kernel
+    (2, 16, 4, 130, 64, "bf16"),   # groups of 4, two row tiles
+    (1, 64, 8, 200, 128, "bf16"),  # groups of 8
+    (4, 8, 2, 257, 96, "f16"),     # groups of 4, register-staged kernel (head dim 96)
+    (1, 16, 8, 900, 128, "f16"),   # small causal grid: pair kernel with groups of 2
+    (3, 12, 4, 150, 64, "f16"),    # 12 groups: not a multiple of 8, plain order
+])
+def test_xcd_group_order(hip, B, Hq, Hkv, S, D, dtype):
+    """Workgroups are dealt to XCDs by (batch, KV head) group when the group count divides by
+    eight; every (row tile, head) must still be computed exactly once."""
+    for j, causal in enumerate([False, True]):
+        _case(dtype, causal, B, Hq, Hkv, S, S, D, 88000 + 97 * Hq + S + j)
