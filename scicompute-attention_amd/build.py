@@ -44,11 +44,6 @@ HIP_FLAGS = [
     "-I" + CSRC_DIR,
 ]
 
-# A measurement build (SCA_MEASUREMENT_BUILD=1 in the environment at build time) compiles in the
-# kernel-selection overrides read from the environment; the default build has none.
-if os.environ.get("SCA_MEASUREMENT_BUILD") == "1":
-    HIP_FLAGS.append("-DSCA_MEASUREMENT_BUILD")
-
 # Per-file additions. The flash kernel never produces NaN from finite inputs (masked logits are
 # -inf, fully masked rows are handled explicitly), so NaN-preserving max operations are not needed.
 FILE_FLAGS = {"flash_fwd.hip": ["-fno-honor-nans"]}

@@ -907,31 +907,9 @@ __global__ __launch_bounds__(256) void decode_order_kernel(const int32_t* seq_le
     order[2 * rank + 1] = mine;
 }
 
-// The MFMA kernel serves every shape it covers. A measurement build (-DSCA_MEASUREMENT_BUILD)
-// reads SCA_DECODE_MFMA=0 to select the VALU kernels instead; the shipped library ignores it.
-bool MfmaDecodeEnabled() {
-#ifdef SCA_MEASUREMENT_BUILD
-    static const bool enabled = [] {
-        const char* v = std::getenv("SCA_DECODE_MFMA");
-        return v == nullptr || v[0] != '0';
-    }();
-    return enabled;
-#else
-    return true;
-#endif
-}
-
 // One wave per head slot (true) or four waves per slot (false): the caller's slot_waves when
-// set, else one wave per slot for paged KV and four for contiguous KV. A measurement build reads
-// SCA_DECODE_WAVE_HEADS=1/0 to force either over both.
+// set, else one wave per slot for paged KV and four for contiguous KV.
 bool MfmaWaveHeads(bool paged, int32_t slot_waves) {
-#ifdef SCA_MEASUREMENT_BUILD
-    static const int mode = [] {
-        const char* v = std::getenv("SCA_DECODE_WAVE_HEADS");
-        return v == nullptr ? -1 : (v[0] == '0' ? 0 : 1);
-    }();
-    if (mode >= 0) return mode == 1;
-#endif
     if (slot_waves == 1) return true;
     if (slot_waves == kDecodeWaves) return false;
     return paged;
@@ -946,8 +924,7 @@ int LaunchForDim(const sca_decode_params& p, hipStream_t s) {
         while ((int64_t{1} << block_shift) < p.block_size) ++block_shift;
     }
     const bool mfma_ok = !std::is_same_v<E, DecF32> && (D == 64 || D == 128) &&
-                         (!kPaged || (int64_t{1} << block_shift) == p.block_size) &&
-                         MfmaDecodeEnabled();
+                         (!kPaged || (int64_t{1} << block_shift) == p.block_size);
     if constexpr (!std::is_same_v<E, DecF32> && (D == 64 || D == 128)) {
         if (mfma_ok) {
             sca_decode_params q = p;

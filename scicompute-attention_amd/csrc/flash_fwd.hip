@@ -8,12 +8,12 @@
 // out = O / l (0 when l == 0), LSE = m + ln(l) (-inf when l == 0).
 //
 // Three kernels share the formulation below:
-//   * flash_fwd_dma_kernel (head_dim 64 and 128, the serving shapes): K/V tiles DMA'd into LDS,
-//     8 waves per workgroup; described at its definition. It also serves packed variable-length
-//     batches in one launch (a device work list of (sequence, row tile), longest first);
+//   * flash_fwd_wide_kernel (head_dim 64 and 128: every non-causal grid, large causal grids and
+//     packed variable-length batches in one launch): 4 waves of 64 query rows, K/V tiles DMA'd
+//     into LDS; described at its definition;
 //   * flash_fwd_pair_kernel (head_dim 64 and 128, causal grids too small to balance 128-row
-//     tiles): the same DMA pipeline in two 4-wave groups that run a complementary pair of
-//     64-row tiles side by side; described at its definition;
+//     tiles): two 4-wave groups that run a complementary pair of 64-row tiles side by side, each
+//     with its own DMA ring; described at its definition;
 //   * flash_fwd_kernel (head_dim 32, 96, 160, 192, 256): 4 waves = 128 query rows, K/V staged
 //     through registers into a double-buffered LDS ring with V transposed on the way in.
 // Formulation: S^T = K Q^T with v_mfma_f32_32x32x16_{f16,bf16} (A = K rows from LDS, B = Q^T in
@@ -464,49 +464,17 @@ __global__ __launch_bounds__(FlashGeom<D>::THREADS, 1) void flash_fwd_kernel(
 }
 
 // ============================================================================================
-// DMA-pipelined variant for head_dim 64 and 128 (the serving shapes).
+// The DMA pipeline of the head_dim 64 / 128 kernels (pair and wide).
 //
 // K and V tiles go straight from global memory to LDS with buffer loads to LDS (16 bytes per
 // lane, no VGPR staging, no transposition) through a buffer resource bounded at the sequence's
 // last row, so rows past seq_kv read as zero. Loads are issued ahead of their use and retired
 // with explicit vmcnt waits plus one barrier per tile. LDS rows are unpadded; 16-byte chunks are
 // XOR-swizzled per row (SwzK / SwzV) so that both the K reads and the V transpose reads are
-// bank-conflict free. The PV A operand (V^T fragments) comes from
-// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j % 4 of the 8 bytes
-// read by lane 4*i + j/4 (i = 0..3), i.e. one head-dim column over 4 consecutive keys.
+// bank-conflict free. The PV A operand (V^T fragments) comes from ds_read_b64_tr_b16: within each
+// 16-lane group, lane j receives element j % 4 of the 8 bytes read by lane 4*i + j/4 (i = 0..3),
+// i.e. one head-dim column over 4 consecutive keys.
 // ============================================================================================
-// Two shapes, both 8 waves of 32 query rows x 32 keys per tile:
-//   RG = 4, KQ = 2: 128 query rows, 64-key tiles, rings of four K slots and four V slots, one
-//   barrier per pair of tiles (non-causal, large causal grids, varlen);
-//   RG = 2, KQ = 4: 64 query rows, 128-key tiles, three K slots + two V slots (small causal
-//   grids: each workgroup runs the row tiles T-1-t and t one after the other, so every
-//   workgroup gets the same share of the triangle).
-// The KQ waves of a row group split each key tile and are merged once, at the end, through LDS.
-template <int D, int RG, int KQ>
-struct DmaGeom {
-    static_assert((RG == 4 && KQ == 2) || (RG == 2 && KQ == 4), "8 waves per workgroup");
-    static constexpr bool kRing4 = RG == 4;
-    static constexpr int BN = 32 * KQ;            // keys per tile (KQ waves x 32 keys per row group)
-    static constexpr int BM = RG * kRowsPerWave;  // query rows per workgroup
-    static constexpr int WAVES = RG * KQ;
-    static constexpr int THREADS = WAVES * kWave;
-    // Split layout: K slots (3 when five tiles fit the 160 KB of LDS, so K is fetched two steps
-    // ahead), then two V slots.
-    static constexpr int STAGES = kRing4 ? 4 : 2;  // tiles of K (and of V) the ring holds
-    static constexpr int KSL = kRing4 ? 0 : (5 * BN * D * 2 <= 160 * 1024 ? 3 : 2);
-    static constexpr int KS = D / 16;
-    static constexpr int DT = D / 32;
-    static constexpr int CPR = D / 8;             // 16-byte chunks per row
-    static constexpr int TILE_BYTES = BN * D * 2; // one K or V tile
-    static constexpr int IPW = BN * CPR / kWave / WAVES;  // DMA instructions per wave per tile
-    static constexpr int LOADS_PER_TILE = 2 * IPW;        // K + V, per wave
-    static constexpr int MERGE_FLOATS = DT * 16 + 2;
-    static constexpr int MERGE_BYTES = RG * (KQ - 1) * kWave * MERGE_FLOATS * 4;
-    // kRing4: four K slots then four V slots. Otherwise KSL K slots then two V slots.
-    static constexpr int RING_BYTES = (kRing4 ? 8 : KSL + 2) * TILE_BYTES;
-    static constexpr int LDS_BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
-    static_assert(IPW >= 1 && BN * CPR == IPW * kWave * WAVES, "tile must split evenly into DMAs");
-};
 
 // 16-byte-chunk swizzles for 64 LDS banks (a 256-byte bank window):
 //   K: the 32 rows a wave reads in one ds_read_b128 land on 16 distinct 4-bank groups;
@@ -569,44 +537,6 @@ __device__ __forceinline__ float Max16(const floatx16& s) {
     const float c = fmaxf(fmaxf(s[8], s[9]), fmaxf(s[10], s[11]));
     const float d = fmaxf(fmaxf(s[12], s[13]), fmaxf(s[14], s[15]));
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
-}
-
-// Lazy rescale. The common case costs a local maximum and one compare: only when some lane of
-// the wave sees a score above its threshold does the wave exchange the two half-row maxima and
-// move m (to the row maximum, when it exceeds m by more than kRescaleSlack), scaling O and l by
-// 2^(m_old - m_new). The exponentials are then bounded by 2^kRescaleSlack.
-template <int DT>
-__device__ __forceinline__ void RescaleIfGrown(const floatx16& sv, float scale2, float inv_scale2,
-                                               RowState& r, floatx16 (&o)[DT]) {
-    const float lm = Max16(sv);
-    if (__builtin_amdgcn_ballot_w64(lm > r.thr) == 0) return;
-    const float tmax = HalfMax(lm) * scale2;
-    const bool grow = tmax > r.m + kRescaleSlack;
-    const float m_new = grow ? tmax : r.m;
-    const float alpha = grow ? fast_exp2(r.m - m_new) : 1.0f;  // 0 when m was -inf
-    r.m = m_new;
-    r.l *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-    }
-    r.thr = (r.m + kRescaleSlack) * inv_scale2;
-    r.neg_mu = (r.m == neg_inf()) ? 0.0f : -r.m;
-}
-
-// P = 2^(s * scale2 - m) rounded to the input dtype as 8 packed pairs (the B operand of the PV
-// MFMAs), and the rounded weights added to the lane's denominator.
-template <typename M>
-__device__ __forceinline__ void ExpPack(const floatx16& sv, float scale2, RowState& r,
-                                        uint32_t (&pw)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float p0 = fast_exp2(fmaf(sv[2 * i], scale2, r.neg_mu));
-        const float p1 = fast_exp2(fmaf(sv[2 * i + 1], scale2, r.neg_mu));
-        pw[i] = M::pack(p0, p1);
-        r.l = M::sum2(pw[i], r.l);
-    }
 }
 
 // Transposed 8-byte LDS read at byte address addr + OFF. Issued from inline asm so that the
@@ -678,532 +608,6 @@ struct VarlenArgs {
     const int32_t* cu_kv;
     const int32_t* tiles;
 };
-
-template <typename E, int D, int RG, int KQ, bool kCausal, bool kVarlen>
-__global__ __launch_bounds__((DmaGeom<D, RG, KQ>::THREADS), 1) void flash_fwd_dma_kernel(
-    const sca_flash_params p, int num_q_tiles, const VarlenArgs va) {
-    using G = DmaGeom<D, RG, KQ>;
-    constexpr bool kRing4 = G::kRing4;
-    using M = Mfma<E>;
-    using vec8 = typename E::vec8;
-    constexpr int BN = G::BN;
-    constexpr int ROW_BYTES = D * 2;
-    constexpr int BM = G::BM;
-    // Slot offsets are DS immediates (the V ring's base lives in the per-lane offsets).
-    static_assert(kRing4 ? 3 * G::TILE_BYTES < 65536 : 2 * G::TILE_BYTES <= 65536,
-                  "slot offsets must fit the 16-bit DS immediate");
-
-    extern __shared__ __align__(16) uint8_t lds8[];
-
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int lane = tid % kWave;
-    const int rg = wave % RG;
-    const int kh = wave / RG;
-
-    const int64_t bh_count = p.batch * p.num_heads;
-    int64_t tile_linear, bh;
-    XcdOrder(p, bh_count, &tile_linear, &bh);
-    const int64_t b = bh / p.num_heads;
-    const int64_t h = bh % p.num_heads;
-    const int64_t h_kv = h / (p.num_heads / p.num_kv_heads);
-    // Sequence geometry: the b-th sequence of the batch, or for a packed varlen launch the
-    // sequence and row tile of work entry tile_linear (tok_*: its first token in the packing).
-    int64_t tok_q = 0, tok_kv = 0, var_qt = 0;
-    int wg_seq_q = static_cast<int>(p.seq_q);
-    int wg_seq_kv = static_cast<int>(p.seq_kv);
-    int wg_diag = static_cast<int>(p.diagonal);
-    if constexpr (kVarlen) {
-        const int seq = va.tiles[2 * tile_linear];
-        var_qt = va.tiles[2 * tile_linear + 1];
-        tok_q = va.cu_q[seq];
-        tok_kv = va.cu_kv[seq];
-        wg_seq_q = va.cu_q[seq + 1] - static_cast<int>(tok_q);
-        wg_seq_kv = va.cu_kv[seq + 1] - static_cast<int>(tok_kv);
-        wg_diag = kCausal ? wg_seq_kv - wg_seq_q : 0;
-    }
-    // Causal split-slot workgroups run row tiles t = tile_linear and T-1-t (largest first).
-    constexpr bool kPaired = kCausal && !kRing4;
-    const int passes = kPaired ? ((2 * tile_linear + 1 < num_q_tiles) ? 2 : 1) : 1;
-    // One row tile, start to finish (called once, or twice for a causal pair).
-    // Query fragments of the current row tile (lane (lr, hh): row lr of the wave, k-step ks
-    // elements 16*ks + 8*hh .. +8; zero past seq_q).
-    vec8 qf[G::KS];
-    auto load_q = [&](const int64_t qt_l, const int lane_l) __attribute__((always_inline)) {
-        const int row = static_cast<int>(qt_l) * BM + rg * kRowsPerWave + (lane_l & 31);
-        const uint16_t* q_row = static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh +
-                                (tok_q + row) * p.q_ss + 8 * (lane_l >> 5);
-#pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks) {
-            uint4 raw = make_uint4(0, 0, 0, 0);
-            if (row < wg_seq_q) raw = *reinterpret_cast<const uint4*>(q_row + 16 * ks);
-            qf[ks] = __builtin_bit_cast(vec8, raw);
-        }
-    };
-    // One row tile, start to finish. kOwnQ: the tile loads its own queries (else they were
-    // loaded by the previous tile); next_qt >= 0: the next tile's queries are loaded once this
-    // tile's DMAs have drained, so their latency hides behind the merge and the output stores.
-    // No wait follows a Q load: the Q loads are older than every tile DMA, so each vmcnt wait
-    // that retires a tile also retires them, and the first QK waits for them by itself.
-    auto run_tile = [&]<bool kOwnQ>(const int64_t qt_in, const int64_t next_qt)
-                        __attribute__((always_inline)) {
-    // The lane index and the tile go through an empty asm so that nothing of this tile's setup
-    // (DMA offsets, fragment addresses) is hoisted above the previous tile's epilogue, where it
-    // would only add register pressure.
-    int lane_v = lane;
-    int64_t qt = qt_in;
-    asm volatile("" : "+v"(lane_v), "+s"(qt));
-    const int lane = lane_v;
-    const int lr = lane & 31;
-    const int hh = lane >> 5;
-    const int q0 = static_cast<int>(qt) * BM;
-    const int wave_q0 = q0 + rg * kRowsPerWave;
-    const int my_q = wave_q0 + lr;
-    const int seq_q = wg_seq_q;
-    const int seq_kv = wg_seq_kv;
-    const int diag = wg_diag;
-
-    const uint8_t* k_bytes = reinterpret_cast<const uint8_t*>(
-        static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh + tok_kv * p.k_ss);
-    const uint8_t* v_bytes = reinterpret_cast<const uint8_t*>(
-        static_cast<const uint16_t*>(p.v) + b * p.v_sb + h_kv * p.v_sh + tok_kv * p.v_ss);
-    const int k_row_bytes = static_cast<int>(p.k_ss) * 2;
-    const int v_row_bytes = static_cast<int>(p.v_ss) * 2;
-
-    if constexpr (kOwnQ) load_q(qt, lane);
-
-    int n_tiles = (seq_kv + BN - 1) / BN;
-    int n_plain = seq_kv / BN;
-    if (kCausal) {
-        const int last_key = q0 + BM - 1 + diag;
-        const int causal_tiles = last_key < 0 ? 0 : last_key / BN + 1;
-        if (causal_tiles < n_tiles) n_tiles = causal_tiles;
-        const int plain = (q0 + diag + 1) / BN;
-        if (plain < n_plain) n_plain = plain;
-    }
-    if (n_plain > n_tiles) n_plain = n_tiles;
-
-    // ---- DMA through buffer resources: base = this (b, kv head), num_records covers the rows
-    //      that exist, so rows past seq_kv (tail tile, or tiles past the end) read as zero and
-    //      need no clamping; every wave issues the same number of DMAs per tile.
-    //      Instruction i of this wave fills bytes [(wave*IPW + i)*1024, +1024) of a tile; lane L
-    //      brings flat chunk P = (wave*IPW + i)*64 + L, i.e. row P / CPR, position P % CPR, which
-    //      holds logical chunk position ^ swizzle(row).
-    const int k_records = (seq_kv - 1) * k_row_bytes + ROW_BYTES;
-    const int v_records = (seq_kv - 1) * v_row_bytes + ROW_BYTES;
-    uint32_t dma_koff[G::IPW], dma_voff[G::IPW];
-#pragma unroll
-    for (int i = 0; i < G::IPW; ++i) {
-        const int P = (wave * G::IPW + i) * kWave + lane;
-        const int row = P / G::CPR;
-        const int pos = P % G::CPR;
-        dma_koff[i] = row * k_row_bytes + (pos ^ SwzK<D>(row)) * 16;
-        dma_voff[i] = row * v_row_bytes + (pos ^ SwzV<D>(row)) * 16;
-    }
-
-    // LDS homes of tile t's K and V: K slots first (RG = 4: four, slot t & 3; RG = 2: KSL, slot
-    // t % KSL), then the V slots (RG = 4: four, slot t & 3; RG = 2: two, slot t & 1).
-    auto v_home = [&]<int S>() -> uint8_t* {
-        return lds8 + ((kRing4 ? 4 : G::KSL) + S) * G::TILE_BYTES;
-    };
-    // K tile t goes to K slot `slot` (tracked by the caller).
-    auto issue_k = [&](int slot, int t) {
-        uint8_t* k_dst = lds8 + slot * G::TILE_BYTES + wave * G::IPW * 1024;
-        const uint32_t k_tile_off = static_cast<uint32_t>(t * BN * k_row_bytes);
-#pragma unroll
-        for (int i = 0; i < G::IPW; ++i) {
-            DmaToLds(k_bytes, k_records, k_dst + i * 1024, dma_koff[i], k_tile_off);
-        }
-    };
-    auto issue_v = [&]<int S>(int t) {
-        uint8_t* v_dst = v_home.template operator()<S>() + wave * G::IPW * 1024;
-        const uint32_t v_tile_off = static_cast<uint32_t>(t * BN * v_row_bytes);
-#pragma unroll
-        for (int i = 0; i < G::IPW; ++i) {
-            DmaToLds(v_bytes, v_records, v_dst + i * 1024, dma_voff[i], v_tile_off);
-        }
-    };
-    floatx16 o[G::DT];
-#pragma unroll
-    for (int dt = 0; dt < G::DT; ++dt) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
-    }
-    float m_used = neg_inf();
-    float l_run = 0.0f;
-    const float scale2 = p.scale * kLog2e;
-
-    const int wkey_base = 32 * kh;
-    // K fragment of k-step ks: row wkey_base + lr, logical chunk 2*ks + hh (= 2*ks ^ hh).
-    const int k_row = wkey_base + lr;
-    uint32_t k_frag[G::KS];
-#pragma unroll
-    for (int ks = 0; ks < G::KS; ++ks) {
-        k_frag[ks] = k_row * ROW_BYTES + (((2 * ks) ^ hh ^ SwzK<D>(k_row)) * 16);
-    }
-    // V^T transpose read of (dt, ps, r): source key v_key + 16*ps + 8*r, head-dim chunk
-    // 4*dt + v_chunk (swizzled), half v_half. The swizzle only depends on key bits the
-    // (16*ps + 8*r) step does not touch, so each dt has one lane offset.
-    const int grp = lane >> 4;
-    const int sl = lane & 15;
-    const int v_key = wkey_base + 4 * hh + (sl >> 2);
-    const int v_chunk = 2 * (grp & 1) + ((sl & 3) >> 1);
-    const int v_half = (sl & 1) * 8;
-    uint32_t v_frag[G::DT];
-#pragma unroll
-    for (int dt = 0; dt < G::DT; ++dt) {
-        // The V slots of the split layout start 2 tiles in; that base lives in the per-lane
-        // offset so the slot offset stays a DS immediate.
-        v_frag[dt] = (kRing4 ? 4 : G::KSL) * G::TILE_BYTES + v_key * ROW_BYTES +
-                     (((4 * dt + v_chunk) ^ SwzV<D>(v_key)) * 16) + v_half;
-    }
-
-    auto qk_at = [&](const uint8_t* base) {
-        vec8 a[G::KS];
-#pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks) a[ks] = *reinterpret_cast<const vec8*>(base + k_frag[ks]);
-        floatx16 acc;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks) acc = M::mma(a[ks], qf[ks], acc);
-        return acc;
-    };
-    auto qk_slot = [&](int slot) { return qk_at(lds8 + slot * G::TILE_BYTES); };
-
-    // P V^T for one key tile: V^T fragments from the V tile at vbase, P from pw (8 packed pairs).
-    auto pv_at = [&](const uint8_t* vbase, const uint32_t (&pw)[8]) {
-        const vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-        const vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
-        vec8 va[G::DT][2];
-#pragma unroll
-        for (int dt = 0; dt < G::DT; ++dt) {
-#pragma unroll
-            for (int ps = 0; ps < 2; ++ps) {
-                const uint2 lo = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps) * ROW_BYTES);
-                const uint2 hi = TrRead<E>::read(vbase + v_frag[dt] + (16 * ps + 8) * ROW_BYTES);
-                va[dt][ps] = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-            }
-        }
-#pragma unroll
-        for (int dt = 0; dt < G::DT; ++dt) {
-            o[dt] = M::mma(va[dt][0], pb0, o[dt]);
-            o[dt] = M::mma(va[dt][1], pb1, o[dt]);
-        }
-        // V^T fragments for two O tiles at a time ahead of their MFMAs
-#pragma unroll
-        for (int dt = 0; dt < G::DT; dt += 2) {
-            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
-        }
-    };
-
-    // One pipeline step for tile j: QK MFMAs of tile j+1 interleaved with the softmax VALU of
-    // tile j, the O rescale when some lane's running max moved, then PV of tile j; then retire
-    // the tiles the next step needs and sync.
-    // RG = 4 (S = j & 3; K slots and V slots are rings of four): steps go in pairs with one
-    // barrier per pair. The even step issues K(j+3), K(j+4) into the slots K(j-1), K(j) left and
-    // V(j+2), V(j+3) into the slots V(j-2), V(j-1) left (all read before the previous pair's
-    // barrier); the odd step retires them and syncs.
-    // Split layout (S = j & 1): V of tile j+1 goes to the slot V(j-1) left and K of tile
-    // j+KSL to the slot K(j) left (read by the previous step's QK). V(j+1) and K(j+2) must land
-    // by the end of this step; with three K slots K(j+3) may stay in flight.
-    // kMaskable && masked: the tile reaches past the causal diagonal or the end of the keys
-    // (`masked` is uniform; kMaskable = false compiles the plain step).
-    auto step = [&]<bool kMaskable, int S>(int j, floatx16& s_in, floatx16& s_out, bool masked) {
-        // Tiles past the last one are not fetched (uniform; the plain steps of the ring loop are
-        // never that close to the end).
-        const bool more_k = !kMaskable || j + G::KSL < n_tiles;  // split layout
-        const bool more_v = !kMaskable || j + 1 < n_tiles;
-        if constexpr (kRing4) {
-            if constexpr ((S & 1) == 0) {
-                if (!kMaskable || j + 3 < n_tiles) issue_k((S + 3) & 3, j + 3);
-                if (!kMaskable || j + 4 < n_tiles) issue_k(S, j + 4);
-                if (!kMaskable || j + 2 < n_tiles) issue_v.template operator()<(S + 2) & 3>(j + 2);
-                if (!kMaskable || j + 3 < n_tiles) issue_v.template operator()<(S + 3) & 3>(j + 3);
-            }
-            s_out = qk_slot((S + 1) & 3);
-        } else {
-            if (more_v) issue_v.template operator()<S ^ 1>(j + 1);
-            if (more_k) issue_k(j % G::KSL, j + G::KSL);
-            s_out = qk_slot((j + 1) % G::KSL);
-        }
-        floatx16 sv = s_in;
-        if (kMaskable && masked) {
-            const int lim = kCausal ? min(seq_kv - 1, my_q + diag) : seq_kv - 1;
-            const int kbase = j * BN + wkey_base + 4 * hh;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int key = kbase + 8 * (i / 4) + (i % 4);
-                sv[i] = key > lim ? neg_inf() : sv[i];
-            }
-        }
-        float tmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                           fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(sv[8], sv[9]), fmaxf(sv[10], sv[11])),
-                                 fmaxf(fmaxf(sv[12], sv[13]), fmaxf(sv[14], sv[15]))));
-        tmax = HalfMax(tmax) * scale2;
-        const bool grow = tmax > m_used + kRescaleSlack;
-        const float m_new = grow ? tmax : m_used;
-        const float alpha = grow ? fast_exp2(m_used - m_new) : 1.0f;
-        m_used = m_new;
-        l_run *= alpha;
-        const float mu = (m_used == neg_inf()) ? 0.0f : m_used;
-        uint32_t pw[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float p0 = fast_exp2(fmaf(sv[2 * i], scale2, -mu));
-            const float p1 = fast_exp2(fmaf(sv[2 * i + 1], scale2, -mu));
-            pw[i] = M::pack(p0, p1);
-            l_run = M::sum2(pw[i], l_run);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(pw[i]));
-        // K fragments in two halves (bounds the live registers), MFMAs spread over the VALU work
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, G::KS / 2, 0);
-#pragma unroll
-        for (int i = 0; i < G::KS; ++i) {
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedValu, 10, 0);
-            if (i == 0) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, G::KS - G::KS / 2, 0);
-        }
-
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-#pragma unroll
-            for (int dt = 0; dt < G::DT; ++dt) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-            }
-        }
-
-        pv_at(lds8 + S * G::TILE_BYTES, pw);
-
-        // Publish the tiles that landed, and make sure every wave is done with the LDS this step
-        // read before the next step refills it.
-        // RG = 4: the odd step of a pair retires the pair's DMAs. Split layout: the DMAs this
-        // step issued may stay in flight (with three K slots, only K(j+3)).
-        if constexpr (kRing4) {
-            if constexpr ((S & 1) == 0) return;
-            WaitVm<0>();
-        } else if constexpr (G::KSL == 3) {
-            if (more_k) {
-                WaitVm<G::IPW>();
-            } else {
-                WaitVm<0>();
-            }
-        } else {
-            WaitVm<0>();
-        }
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-        __builtin_amdgcn_s_barrier();
-    };
-
-    if constexpr (kRing4) {
-        issue_k(0, 0);
-        issue_k(1, 1);
-        issue_v.template operator()<0>(0);
-        issue_k(2, 2);
-        issue_v.template operator()<1>(1);
-        WaitVm<4 * G::IPW>();  // K(0) landed; the first QK runs while the rest arrive
-        __builtin_amdgcn_s_barrier();
-        floatx16 s0 = qk_slot(0), s1;
-        // Every wave has read K(0) before step 0 refills its slot with K(4); K(1), V(0), K(2),
-        // V(1) are published by the same barrier.
-        WaitVm<0>();
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-        __builtin_amdgcn_s_barrier();
-        int j = 0;
-        // Steady state: four steps per trip, slots fixed at compile time, scores ping-pong.
-        for (; j + 4 <= n_plain; j += 4) {
-            step.template operator()<false, 0>(j, s0, s1, false);
-            step.template operator()<false, 1>(j + 1, s1, s0, false);
-            step.template operator()<false, 2>(j + 2, s0, s1, false);
-            step.template operator()<false, 3>(j + 3, s1, s0, false);
-        }
-        // Remaining plain tiles and the boundary tiles (masking a fully visible tile is harmless).
-        for (; j < n_tiles; ++j) {
-            switch (j & 3) {
-                case 0: step.template operator()<true, 0>(j, s0, s1, true); break;
-                case 1: step.template operator()<true, 1>(j, s0, s1, true); break;
-                case 2: step.template operator()<true, 2>(j, s0, s1, true); break;
-                default: step.template operator()<true, 3>(j, s0, s1, true); break;
-            }
-            s0 = s1;
-        }
-    } else {
-        floatx16 s0, s1;
-        int j = 0;
-        issue_k(0, 0);
-        issue_k(1, 1);
-        issue_v.template operator()<0>(0);
-        if constexpr (G::KSL == 3) {
-            issue_k(2, 2);
-            WaitVm<3 * G::IPW>();  // K(0) landed; the first QK runs while the rest arrive
-        } else {
-            WaitVm<2 * G::IPW>();
-        }
-        __builtin_amdgcn_s_barrier();
-        s0 = qk_slot(0);
-        // Every wave has read K(0) before step 0 refills its slot; K(1) and V(0) are published
-        // by the same barrier (K(2) may stay in flight).
-        if constexpr (G::KSL == 3) {
-            WaitVm<G::IPW>();
-        } else {
-            WaitVm<0>();
-        }
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-        __builtin_amdgcn_s_barrier();
-        // Two steps per trip (stages fixed at compile time); tiles from n_plain on are masked
-        // through a uniform flag, so the boundary tiles stay in the same code path.
-        for (; j + 2 <= n_tiles; j += 2) {
-            step.template operator()<true, 0>(j, s0, s1, j >= n_plain);
-            step.template operator()<true, 1>(j + 1, s1, s0, j + 1 >= n_plain);
-        }
-        if (j < n_tiles) step.template operator()<true, 0>(j, s0, s1, j >= n_plain);
-    }
-
-    // Drain the trailing DMAs before the LDS is reused for the merge (or released).
-    WaitVm<0>();
-    __builtin_amdgcn_s_barrier();
-    if (next_qt >= 0) load_q(next_qt, lane);
-
-    // Merge the KQ key-slices of every row group into the kh == 0 wave. Buffer of wave (kh, rg):
-    // O as 16-byte quads, quad k of lane L at ((kh-1)*RG + rg) * 4*DT*64 + k*64 + L (lane-major,
-    // so every access is a conflict-free 16-byte one), then (m, l) pairs at the end.
-    {
-        float4* const mquad = reinterpret_cast<float4*>(lds8);
-        float2* const mstat = reinterpret_cast<float2*>(mquad + (KQ - 1) * RG * 4 * G::DT * kWave);
-        if (kh != 0) {
-            float4* mbuf = mquad + ((kh - 1) * RG + rg) * 4 * G::DT * kWave + lane;
-#pragma unroll
-            for (int dt = 0; dt < G::DT; ++dt) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    mbuf[(4 * dt + g) * kWave] = make_float4(o[dt][4 * g], o[dt][4 * g + 1],
-                                                             o[dt][4 * g + 2], o[dt][4 * g + 3]);
-                }
-            }
-            mstat[((kh - 1) * RG + rg) * kWave + lane] = make_float2(m_used, l_run);
-        }
-        __syncthreads();
-        if (kh == 0) {
-            // One maximum over the KQ states, then every O tile scaled and accumulated 16 values
-            // at a time (keeps the merge inside the register budget).
-            const float4* mbuf0 = mquad + rg * 4 * G::DT * kWave + lane;
-            constexpr int kStride = RG * 4 * G::DT * kWave;  // quads between the KQ-1 buffers
-            float2 st[KQ];
-#pragma unroll
-            for (int q = 1; q < KQ; ++q) st[q] = mstat[((q - 1) * RG + rg) * kWave + lane];
-            float mm = m_used;
-#pragma unroll
-            for (int q = 1; q < KQ; ++q) mm = fmaxf(mm, st[q].x);
-            float wq[KQ];
-            wq[0] = (m_used == neg_inf()) ? 0.0f : fast_exp2(m_used - mm);
-            l_run *= wq[0];
-#pragma unroll
-            for (int q = 1; q < KQ; ++q) {
-                wq[q] = (st[q].x == neg_inf()) ? 0.0f : fast_exp2(st[q].x - mm);
-                l_run += st[q].y * wq[q];
-            }
-            m_used = mm;
-            if constexpr (!kRing4) {
-                // Split layout: each O tile is merged and written out before the next one is
-                // touched (the paired passes leave no registers for a merged copy of O).
-                const float l_tot = HalfSum(l_run);
-                const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-                const bool row_ok = my_q < seq_q;
-                uint16_t* out_row = static_cast<uint16_t*>(p.out) + b * p.o_sb + h * p.o_sh +
-                                    (tok_q + my_q) * p.o_ss;
-#pragma unroll
-                for (int dt = 0; dt < G::DT; ++dt) {
-                    float acc[16];
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) acc[i] = o[dt][i] * wq[0];
-#pragma unroll
-                    for (int q = 1; q < KQ; ++q) {
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            const float4 v = mbuf0[(q - 1) * kStride + (4 * dt + g) * kWave];
-                            acc[4 * g] += v.x * wq[q];
-                            acc[4 * g + 1] += v.y * wq[q];
-                            acc[4 * g + 2] += v.z * wq[q];
-                            acc[4 * g + 3] += v.w * wq[q];
-                        }
-                    }
-                    if (row_ok) {
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            const int d0 = 32 * dt + 8 * g + 4 * hh;
-                            const uint32_t lo = M::pack(acc[4 * g + 0] * inv, acc[4 * g + 1] * inv);
-                            const uint32_t hi = M::pack(acc[4 * g + 2] * inv, acc[4 * g + 3] * inv);
-                            *reinterpret_cast<uint2*>(out_row + d0) = make_uint2(lo, hi);
-                        }
-                    }
-                }
-                if (row_ok && p.lse != nullptr && hh == 0) {
-                    p.lse[(b * p.num_heads + h) * p.seq_q + my_q] =
-                        l_tot > 0.0f ? (m_used + __log2f(l_tot)) * kLn2 : neg_inf();
-                }
-            } else {
-#pragma unroll
-            for (int dt = 0; dt < G::DT; ++dt) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[dt][i] *= wq[0];
-#pragma unroll
-                for (int q = 1; q < KQ; ++q) {
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const float4 v = mbuf0[(q - 1) * kStride + (4 * dt + g) * kWave];
-                        o[dt][4 * g] += v.x * wq[q];
-                        o[dt][4 * g + 1] += v.y * wq[q];
-                        o[dt][4 * g + 2] += v.z * wq[q];
-                        o[dt][4 * g + 3] += v.w * wq[q];
-                    }
-                }
-                __builtin_amdgcn_sched_barrier(0);  // one O tile's LDS reads in flight at a time
-            }
-            }
-        }
-    }
-    if (kRing4 && kh == 0) {
-
-    const float l_tot = HalfSum(l_run);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (my_q < seq_q) {
-        uint16_t* out_row = static_cast<uint16_t*>(p.out) + b * p.o_sb + h * p.o_sh +
-                            (tok_q + my_q) * p.o_ss;
-#pragma unroll
-        for (int dt = 0; dt < G::DT; ++dt) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d0 = 32 * dt + 8 * g + 4 * hh;
-                const uint32_t lo = M::pack(o[dt][4 * g + 0] * inv, o[dt][4 * g + 1] * inv);
-                const uint32_t hi = M::pack(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
-                *reinterpret_cast<uint2*>(out_row + d0) = make_uint2(lo, hi);
-            }
-        }
-        if (p.lse != nullptr && hh == 0) {
-            p.lse[(b * p.num_heads + h) * p.seq_q + my_q] =
-                l_tot > 0.0f ? (m_used + __log2f(l_tot)) * kLn2 : neg_inf();
-        }
-    }
-    }  // kh == 0
-    };  // run_tile
-
-    if constexpr (kPaired) {
-        run_tile.template operator()<true>(num_q_tiles - 1 - tile_linear,
-                                           passes == 2 ? tile_linear : -1);
-        if (passes == 2) {
-            __syncthreads();  // the first tile's merge buffer is the second tile's ring
-            run_tile.template operator()<false>(tile_linear, -1);
-        }
-    } else if constexpr (kVarlen) {
-        run_tile.template operator()<true>(var_qt, -1);
-    } else {
-        run_tile.template operator()<true>(kCausal ? num_q_tiles - 1 - tile_linear : tile_linear,
-                                           -1);
-    }
-}
 
 // ---- Two-group causal pair kernel ---------------------------------------------------------------
 // Small causal grids: each workgroup owns the complementary 64-row tiles A = T-1-t (long) and
@@ -1402,6 +806,74 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
     auto run_keys = [&](int qt, int kb, int ke, int n_plain) {
         if (kb >= ke) return;
         const int my_q = qt * BM + rg * 32 + lr;
+        const int lim = min(seq_kv - 1, my_q + diag);
+        // Keys above lim_j read as -inf (lim_j = -1 masks the whole tile: the score tile past
+        // the range's end is computed from a stale slot and must not move the maximum).
+        auto mask = [&](int jt, int lim_j, floatx16& sv) {
+            const int kbase = jt * BN + wkey_base + 4 * hh;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kbase + 8 * (i / 4) + (i % 4);
+                sv[i] = key > lim_j ? neg_inf() : sv[i];
+            }
+        };
+        // Scores of one tile -> exponent arguments in place (t = s * scale2 - m), the first
+        // half's weights (keys of pw[0..3]) and their sum. Returns the lane's raw maximum.
+        auto prep = [&](floatx16& sv, uint32_t (&ph)[4], float& sh) {
+            const float lm = Max16(sv);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sv[i] = fmaf(sv[i], scale2, rs.neg_mu);
+            float a = 0.0f, c = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p0 = fast_exp2(sv[2 * i]);
+                const float p1 = fast_exp2(sv[2 * i + 1]);
+                ph[i] = M::pack(p0, p1);
+                a += p0;
+                c += p1;
+            }
+            sh = a + c;
+            // Pinned here: otherwise they sink below the rare rescale branch, out of PV's shadow.
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(ph[i]));
+            asm volatile("" : "+v"(sh));
+            return lm;
+        };
+        // Lazy rescale, decided after prep ran with the current maximum: only when some lane of
+        // the wave sees a raw score above its threshold does the wave exchange the two half-row
+        // maxima and move m (to the row maximum, when it exceeds m by more than kRescaleSlack),
+        // scaling O and l by 2^(m_old - m_new); the tile's exponent arguments and first-half
+        // weights are then redone. The exponentials stay bounded by 2^kRescaleSlack.
+        auto fix = [&](float lm, floatx16& sv, uint32_t (&ph)[4], float& sh) {
+            if (__builtin_amdgcn_ballot_w64(lm > rs.thr) == 0) return;
+            const float tmax = HalfMax(lm) * scale2;
+            const bool grow = tmax > rs.m + kRescaleSlack;
+            const float m_new = grow ? tmax : rs.m;
+            const float alpha = grow ? fast_exp2(rs.m - m_new) : 1.0f;
+            const float neg_mu_new = (m_new == neg_inf()) ? 0.0f : -m_new;
+            const float delta = neg_mu_new - rs.neg_mu;
+            rs.m = m_new;
+            rs.l *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < G::DT; ++dt) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+            }
+            rs.thr = (rs.m + kRescaleSlack) * inv_scale2;
+            rs.neg_mu = neg_mu_new;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sv[i] += delta;
+            float a = 0.0f, c = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p0 = fast_exp2(sv[2 * i]);
+                const float p1 = fast_exp2(sv[2 * i + 1]);
+                ph[i] = M::pack(p0, p1);
+                a += p0;
+                c += p1;
+            }
+            sh = a + c;
+        };
         // Prologue: K(kb), K(kb+1), V(kb); QK(kb) once K(kb) has landed.
         issue_k(kb);
         if (kb + 1 < ke) issue_k(kb + 1);
@@ -1413,23 +885,23 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
         }
         gsync();
         floatx16 s_cur = qk_slot(kb & 1);
+        uint32_t ph_cur[4];
+        float sh_cur;
+        if (kb >= n_plain) mask(kb, lim, s_cur);
+        {
+            const float lm = prep(s_cur, ph_cur, sh_cur);
+            fix(lm, s_cur, ph_cur, sh_cur);
+        }
         WaitVm<0>();
         gsync();  // K(kb) read by every wave before step kb refills its slot
         // Step j (S = j & 1): K(j+2) into K slot S and V(j+1) into V slot S^1 (both read in
-        // step j-1), QK(j+1) from K slot S^1 under the softmax of tile j, PV(j) from V slot S;
-        // then everything issued has landed before the group barrier. V's DMAs are issued
-        // behind the K fragment reads of QK(j+1), so those start sooner (2-3% faster than
-        // issuing both tiles first).
-        // Instruction order inside a step (each wave): V^T fragments of tile j and K fragments
-        // of tile j+1 are read first (nothing is in flight yet, so they start at once), then the
-        // step's DMAs go out; the masking and the local row maximum decide whether the rare
-        // rescale runs; the 8 QK MFMAs of tile j+1 are then interleaved one per 6 instructions
-        // of the exponentials of tile j, so the wave's VALU work issues while its MFMAs run;
-        // the PV MFMAs of tile j close the step. The QK of the last step reads a stale K slot
-        // (its result is unused), which keeps the step free of branches around the MFMAs.
-        auto step = [&]<int S>(int j, floatx16& s_in, floatx16& s_out) {
-            vec8 va[2 * G::DT];
-            ReadVFrags<(2 + S) * G::TILE_BYTES, ROW_BYTES>(v_addr, va);
+        // step j-1), QK(j+1) from K slot S^1, PV(j) from V slot S. The softmax work is split
+        // between the two MFMA runs of the step so that each has VALU and transcendental work
+        // to hide: under QK(j+1) the second half of tile j's weights; under PV(j) tile j+1's
+        // maximum, exponent arguments and first-half weights (with the current maximum; the
+        // rare move of the maximum redoes them after PV).
+        auto step = [&]<int S, bool MASK>(int j, floatx16& s_in, uint32_t (&ph_in)[4], float sh_in,
+                                          floatx16& s_out, uint32_t (&ph_out)[4], float& sh_out) {
             vec8 kf[G::KS];
             {
                 const uint8_t* base = lds8 + (S ^ 1) * G::TILE_BYTES;
@@ -1438,27 +910,37 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
                     kf[ks] = *reinterpret_cast<const vec8*>(base + k_frag[ks]);
                 }
             }
+            vec8 va[2 * G::DT];
+            ReadVFrags<(2 + S) * G::TILE_BYTES, ROW_BYTES>(v_addr, va);
             if (j + 2 < ke) issue_k(j + 2);
             if (j + 1 < ke) issue_v(j + 1);
-            floatx16 sv = s_in;
-            if (j >= n_plain) {
-                const int lim = min(seq_kv - 1, my_q + diag);
-                const int kbase = j * BN + wkey_base + 4 * hh;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = kbase + 8 * (i / 4) + (i % 4);
-                    sv[i] = key > lim ? neg_inf() : sv[i];
-                }
-            }
-            RescaleIfGrown(sv, scale2, inv_scale2, rs, o);
             uint32_t pw[8];
-            ExpPack<M>(sv, scale2, rs, pw);
+            {
+                float a = 0.0f, c = 0.0f;
+#pragma unroll
+                for (int i = 4; i < 8; ++i) {
+                    const float p0 = fast_exp2(s_in[2 * i]);
+                    const float p1 = fast_exp2(s_in[2 * i + 1]);
+                    pw[i] = M::pack(p0, p1);
+                    a += p0;
+                    c += p1;
+                }
+                rs.l += sh_in + (a + c);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pw[i] = ph_in[i];
             floatx16 acc;
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
             for (int ks = 0; ks < G::KS; ++ks) acc = M::mma(kf[ks], qf[ks], acc);
             s_out = acc;
+#pragma unroll
+            for (int i = 0; i < G::KS; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSchedValuTrans, 3, 0);
+            }
+            if constexpr (MASK) mask(j + 1, j + 1 < ke ? lim : -1, s_out);
             vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
             vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
             WaitLdsTied(va, pb0, pb1);
@@ -1467,30 +949,48 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
                 o[dt] = M::mma(va[2 * dt], pb0, o[dt]);
                 o[dt] = M::mma(va[2 * dt + 1], pb1, o[dt]);
             }
+            const float lm = prep(s_out, ph_out, sh_out);
 #pragma unroll
-            for (int i = 0; i < G::KS; ++i) {
+            for (int i = 0; i < 2 * G::DT; ++i) {
                 __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSchedValuTrans, 48 / G::KS, 0);
+                __builtin_amdgcn_sched_group_barrier(kSchedValuTrans, 6, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * G::DT, 0);
             __builtin_amdgcn_sched_barrier(0);
+            fix(lm, s_out, ph_out, sh_out);
             WaitVm<0>();
             gsync();
         };
         floatx16 s_next;
+        uint32_t ph_next[4];
+        float sh_next;
         int j = kb;
-        if (j & 1) {
-            step.template operator()<1>(j, s_cur, s_next);
-            s_cur = s_next;
-            ++j;
-        }
-        for (; j + 2 <= ke; j += 2) {
-            step.template operator()<0>(j, s_cur, s_next);
-            step.template operator()<1>(j + 1, s_next, s_cur);
-        }
-        if (j < ke) step.template operator()<0>(j, s_cur, s_next);
+        // Steps whose next tile needs no mask, then the rest (the diagonal tile and the range's
+        // end); each run alternates the two register sets and slots by the step's parity.
+        auto run = [&]<bool MASK>(int j_end) {
+            if (j < j_end && (j & 1)) {
+                step.template operator()<1, MASK>(j, s_cur, ph_cur, sh_cur, s_next, ph_next, sh_next);
+                s_cur = s_next;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ph_cur[i] = ph_next[i];
+                sh_cur = sh_next;
+                ++j;
+            }
+            for (; j + 2 <= j_end; j += 2) {
+                step.template operator()<0, MASK>(j, s_cur, ph_cur, sh_cur, s_next, ph_next, sh_next);
+                step.template operator()<1, MASK>(j + 1, s_next, ph_next, sh_next, s_cur, ph_cur, sh_cur);
+            }
+            if (j < j_end) {
+                step.template operator()<0, MASK>(j, s_cur, ph_cur, sh_cur, s_next, ph_next, sh_next);
+                s_cur = s_next;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ph_cur[i] = ph_next[i];
+                sh_cur = sh_next;
+                ++j;
+            }
+        };
+        run.template operator()<false>(min(ke, n_plain) - 1);
+        run.template operator()<true>(ke);
     };
-
     float4* const mquad = reinterpret_cast<float4*>(lds8);
     if (g == 0) {
         load_q(qa);
@@ -1731,31 +1231,6 @@ __device__ __forceinline__ void WaitLgkmTied(V& reg) {
 
 __device__ __forceinline__ void Fence() { __builtin_amdgcn_sched_barrier(0); }
 
-// Ablation mask of the wide kernel's step (measurement builds only; 0 in the shipped library):
-// 1 no PV MFMAs, 2 no QK MFMAs, 4 no exponentials, 8 no V reads, 16 no K reads, 32 no DMAs,
-// 64 no barrier. The results of an ablated build are wrong by construction.
-#if defined(SCA_MEASUREMENT_BUILD) && defined(SCA_ABL)
-constexpr int kAbl = SCA_ABL;
-#else
-constexpr int kAbl = 0;
-#endif
-
-// Region clocks of the wide kernel's steps (measurement builds with SCA_STAMPS only): per wave,
-// the shader cycles spent in each of 8 regions summed over the steps, read back through
-// sca_hip_debug_wide_stamps.
-#if defined(SCA_MEASUREMENT_BUILD) && defined(SCA_STAMPS)
-constexpr bool kStamps = true;
-__device__ uint32_t g_wide_stamps[4096 * 4][9];
-#else
-constexpr bool kStamps = false;
-#endif
-// Issues s_memtime without waiting for it: the value may be read only after an lgkmcnt(0).
-__device__ __forceinline__ uint64_t MemtimeNoWait() {
-    uint64_t v;
-    asm volatile("s_memtime %0" : "=s"(v));
-    return v;
-}
-
 // Gives a value the AGPR register class (an empty asm with an AGPR in/out operand), so that the
 // loop-carried accumulators and Q fragments stay in AGPRs instead of being copied in and out.
 template <typename V>
@@ -1850,7 +1325,7 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
         }
     }
 
-    // ---- DMA (as in the DMA kernel: buffer resources bounded at the last row) ----
+    // ---- DMA (buffer resources bounded at the sequence's last row) ----
     const uint8_t* k_bytes = reinterpret_cast<const uint8_t*>(
         static_cast<const uint16_t*>(p.k) + b * p.k_sb + h_kv * p.k_sh + tok_kv * p.k_ss);
     const uint8_t* v_bytes = reinterpret_cast<const uint8_t*>(
@@ -2045,10 +1520,6 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();
 
-    uint32_t st_acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    uint64_t st_t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    uint64_t st_prev = 0;
-
     // One step for key tile j (S = j & 3, VB = j & 1). On entry S(j) is masked and the rescale
     // for tile j is done, kf holds K(j+1)'s fragments and va[VB] V(j)'s. Four regions, each one
     // MFMA stream with VALU and LDS work placed between its MFMAs:
@@ -2068,7 +1539,6 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
                                            floatx16 (&s_out)[G::RT]) __attribute__((always_inline)) {
         constexpr int VB = S & 1;
         constexpr int NPV = 2 * G::DT;  // PV MFMAs per subtile
-        if constexpr (kStamps) st_t[0] = MemtimeNoWait();
         const bool next_ok = !kMaskable || j + 1 < n_tiles;   // S(j+1) is a real tile
         const bool next_masked = kMaskable && j + 1 >= n_plain;
         uint32_t pw[G::RT][8];
@@ -2084,10 +1554,6 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
                                       12, 13, 26, 27, 36, 42, 43, 14, 15, 28, 29, 37, 44, 45,
                                       30, 31, 46, 47, 38, 39, 48, 49, 50, 51, 52, 53, 54, 55};
             const int c = kOps[n];
-            if (kAbl & 4) {
-                if (c >= 32 && c < 40) pw[r][c - 32] = 0x3c003c00u;
-                return;
-            }
             if (c < 16) {
                 s_in[r][c] = fmaf(s_in[r][c], scale2, rs[r].neg_mu);
             } else if (c < 32) {
@@ -2101,7 +1567,6 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
             }
         };
         auto qk = [&](int r, int ks) __attribute__((always_inline)) {
-            if (kAbl & 2) return;
             if (ks == 0) {
                 A::first_v(s_out[r], kf[0], qf[r][0]);
             } else {
@@ -2114,7 +1579,6 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
             pb[r][1] = __builtin_bit_cast(vec8, make_uint4(pw[r][4], pw[r][5], pw[r][6], pw[r][7]));
         };
         auto pv = [&](int r, int i) __attribute__((always_inline)) {
-            if (kAbl & 1) return;
             A::acc_a(o[r][i / 2], va[VB][i], pb[r][i % 2]);
         };
         // The step's 2*IPW DMA instructions (K(j+4) into K slot S, V(j+3) into V slot S-1),
@@ -2122,7 +1586,6 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
         // g*kDmaPerRegion + i / kDmaSpacing when i is a multiple of kDmaSpacing.
         constexpr int kDmaPerRegion = (2 * G::IPW + 3) / 4;
         auto dma = [&](int g, int i) __attribute__((always_inline)) {
-            if (kAbl & 32) return;
             constexpr int kSpacing = 8 / kDmaPerRegion > 0 ? 8 / kDmaPerRegion : 1;
             if (i % kSpacing != 0) return;
             const int n = g * kDmaPerRegion + i / kSpacing;
@@ -2147,7 +1610,6 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
         // P operands: 2 wait states after their VALU writes (the compiler does not see the
         // inline-asm MFMA that reads them).
         asm volatile("s_nop 1" : "+v"(pb[0][0]), "+v"(pb[0][1]));
-        if constexpr (kStamps) st_t[1] = MemtimeNoWait();
         // ---- B ----
         constexpr int kVReadsB = 4 * G::DT / NPV;  // V reads per PV MFMA
         constexpr int kOpsB = (28 + NPV - 1) / NPV;  // subtile 1's operations 0-27
@@ -2160,15 +1622,12 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
                 if (i * kOpsB + q < 28) op(1, i * kOpsB + q);
             }
             dma(1, i);
-            if (!(kAbl & 8)) {
 #pragma unroll
-                for (int q = 0; q < kVReadsB; ++q) {
-                    read_v1.template operator()<(S + 1) & 3, VB ^ 1>(i * kVReadsB + q);
-                }
+            for (int q = 0; q < kVReadsB; ++q) {
+                read_v1.template operator()<(S + 1) & 3, VB ^ 1>(i * kVReadsB + q);
             }
             Fence();
         }
-        if constexpr (kStamps) st_t[2] = MemtimeNoWait();
         // ---- C ----
         float lm0 = neg_inf(), lm1 = neg_inf();
         constexpr int kOpsC = (28 + G::KS - 1) / G::KS;  // subtile 1's operations 28-55
@@ -2189,7 +1648,6 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
         pack_p(1);
         // P operands: 2 wait states after their VALU writes.
         asm volatile("s_nop 1" : "+v"(pb[1][0]), "+v"(pb[1][1]));
-        if constexpr (kStamps) st_t[3] = MemtimeNoWait();
         // ---- D ----
 #pragma unroll
         for (int i = 0; i < NPV; ++i) {
@@ -2199,7 +1657,7 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
                 asm volatile("s_nop 4");
                 if (next_ok) lm1 = mask_max(s_out[1], 1, j + 1, next_masked);
             }
-            if (i >= 1 && !(kAbl & 16)) {
+            if (i >= 1) {
                 // KS K reads over the MFMAs 1 .. NPV-1 (kf was last read two MFMAs ago).
                 constexpr int kPer = (G::KS + NPV - 2) / (NPV - 1);
 #pragma unroll
@@ -2222,11 +1680,9 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
             dma(3, i);
             Fence();
         }
-        if constexpr (kStamps) st_t[4] = MemtimeNoWait();
         // ---- rare rescale for tile j+1 ----
         if (next_ok) rescale_if_grown(lm0, lm1);
         Fence();
-        if constexpr (kStamps) st_t[5] = MemtimeNoWait();
         // ---- K(j+3) and V(j+2) landed (at the tail, everything); fragment reads retired ----
         if (!kMaskable || j + 4 < n_tiles) {
             WaitVm<2 * G::IPW>();
@@ -2234,14 +1690,7 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
             WaitVm<0>();
         }
         WaitLgkmTied<0>(kf[G::KS - 1]);
-        if constexpr (kStamps) {
-            st_t[6] = MemtimeNoWait();
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (st_prev != 0) st_acc[7] += static_cast<uint32_t>(st_t[0] - st_prev);
-            for (int k = 0; k < 6; ++k) st_acc[k] += static_cast<uint32_t>(st_t[k + 1] - st_t[k]);
-            st_prev = st_t[6];
-        }
-        if (!(kAbl & 64)) __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_s_barrier();
     };
 
     int j = 0;
@@ -2263,13 +1712,6 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
         step.template operator()<true, 3>(j + 3, s1, s0);
     }
 
-#if defined(SCA_MEASUREMENT_BUILD) && defined(SCA_STAMPS)
-    if (lane == 0 && blockIdx.x < 4096) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) g_wide_stamps[blockIdx.x * 4 + wave][k] = st_acc[k];
-        g_wide_stamps[blockIdx.x * 4 + wave][8] = static_cast<uint32_t>(n_tiles);
-    }
-#endif
     // ---- epilogue: merge the key halves of each row group, normalise, store ----
     WaitVm<0>();
     SettleO(o);
@@ -2364,33 +1806,6 @@ int LaunchFlashWide(const sca_flash_params& p, hipStream_t s) {
 template <typename E, int D, bool kCausal>
 int LaunchFlash(const sca_flash_params& p, hipStream_t s);
 
-template <typename E, int D, int RG, bool kCausal>
-int LaunchFlashDma(const sca_flash_params& p, hipStream_t s) {
-    constexpr int KQ = RG == 4 ? 2 : 4;
-    using G = DmaGeom<D, RG, KQ>;
-    // Buffer offsets are 32-bit: rows up to seq_kv plus a few tiles of overrun must fit.
-    const int64_t extent_k = (p.seq_kv + 4 * G::BN) * p.k_ss * 2;
-    const int64_t extent_v = (p.seq_kv + 4 * G::BN) * p.v_ss * 2;
-    if (extent_k >= (1LL << 31) || extent_v >= (1LL << 31)) return LaunchFlash<E, D, kCausal>(p, s);
-    const int64_t num_q_tiles = (p.seq_q + G::BM - 1) / G::BM;
-    // Causal split-slot workgroups each take a pair of row tiles.
-    const int64_t row_slots = (kCausal && !G::kRing4) ? (num_q_tiles + 1) / 2 : num_q_tiles;
-    const int64_t blocks = row_slots * p.batch * p.num_heads;
-    if (blocks <= 0) return 0;
-    if (blocks > 0x7fffffffLL) {
-        return SetError(SCA_E_SEQ_TOO_LONG, "flash: grid of " + std::to_string(blocks) +
-                                                " workgroups exceeds the launch limit");
-    }
-    if (const int rc =
-            EnsureLdsLimit<&flash_fwd_dma_kernel<E, D, RG, KQ, kCausal, false>>(G::LDS_BYTES, "flash LDS limit")) {
-        return rc;
-    }
-    hipLaunchKernelGGL((flash_fwd_dma_kernel<E, D, RG, KQ, kCausal, false>),
-                       dim3(static_cast<unsigned>(blocks)), dim3(G::THREADS), G::LDS_BYTES, s, p,
-                       static_cast<int>(num_q_tiles), VarlenArgs{nullptr, nullptr, nullptr});
-    return CheckLaunch("flash_fwd_dma_kernel", s);
-}
-
 template <typename E, int D, bool kCausal>
 int LaunchFlash(const sca_flash_params& p, hipStream_t s) {
     using G = FlashGeom<D>;
@@ -2432,35 +1847,12 @@ int LaunchFlashPair(const sca_flash_params& p, hipStream_t s) {
     return CheckLaunch("flash_fwd_pair_kernel", s);
 }
 
-// Small causal grids (64-row tiles in complementary pairs) run the two-group pair kernel. A
-// measurement build (-DSCA_MEASUREMENT_BUILD) reads SCA_FLASH_PAIR=0 to select the 8-wave
-// paired pass kernel instead; the shipped library ignores the variable.
-bool UsePairKernel() {
-#ifdef SCA_MEASUREMENT_BUILD
-    static const bool on = [] {
-        const char* env = std::getenv("SCA_FLASH_PAIR");
-        return env == nullptr || std::atoi(env) != 0;
-    }();
-    return on;
-#else
-    return true;
-#endif
-}
-
-// Row groups of the DMA kernel. Non-causal: 4 (128-row workgroups, the least K/V traffic per
-// FLOP). Causal: 2 (64-row tiles taken in complementary pairs, so every workgroup gets the same
-// share of the triangle) while the pairs fit one workgroup per CU (the pair kernel) or fewer
-// than two per CU (the 8-wave kernel, SCA_FLASH_PAIR=0); beyond that the longest-first 128-row
-// grid balances better. In a measurement build SCA_FLASH_ROW_GROUPS (2 or 4) overrides the
-// choice.
-int DmaRowGroups(const sca_flash_params& p, bool causal) {
-#ifdef SCA_MEASUREMENT_BUILD
-    if (const char* env = std::getenv("SCA_FLASH_ROW_GROUPS")) {
-        const int v = std::atoi(env);
-        if (v == 2 || v == 4) return v;
-    }
-#endif
-    if (!causal) return 4;
+// Causal grids with at most one 128-row tile per CU run the pair kernel (64-row tiles in
+// complementary pairs, so every workgroup holds the same share of the triangle); larger causal
+// grids and every non-causal grid run the wide kernel (longest tiles first when causal). Measured
+// warm: at 320-448 tiles on 256 CUs the longest-first 128-row grid is 20-30% faster than a
+// second partial wave of pairs; at 256 tiles the pairs are 30% faster.
+bool UsePairs(const sca_flash_params& p) {
     static int cu_count = [] {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -2471,10 +1863,7 @@ int DmaRowGroups(const sca_flash_params& p, bool causal) {
         return n > 0 ? n : 256;
     }();
     const int64_t tiles128 = (p.seq_q + 127) / 128 * p.batch * p.num_heads;
-    // One pair per 128-row tile: tiles128 pairs of 64-row tiles.
-    const int64_t pair_limit = UsePairKernel() ? static_cast<int64_t>(cu_count)
-                                               : 2 * static_cast<int64_t>(cu_count) - 1;
-    return tiles128 <= pair_limit ? 2 : 4;
+    return tiles128 <= static_cast<int64_t>(cu_count);
 }
 
 template <typename E, bool kCausal>
@@ -2482,18 +1871,12 @@ int LaunchForDim(const sca_flash_params& p, hipStream_t s) {
     switch (p.head_dim) {
         case 32: return LaunchFlash<E, 32, kCausal>(p, s);
         case 64:
-            if (kCausal && UsePairKernel() && DmaRowGroups(p, kCausal) == 2) {
-                return LaunchFlashPair<E, 64>(p, s);
-            }
-            return DmaRowGroups(p, kCausal) == 2 ? LaunchFlashDma<E, 64, 2, kCausal>(p, s)
-                                                 : LaunchFlashWide<E, 64, kCausal>(p, s);
+            if (kCausal && UsePairs(p)) return LaunchFlashPair<E, 64>(p, s);
+            return LaunchFlashWide<E, 64, kCausal>(p, s);
         case 96: return LaunchFlash<E, 96, kCausal>(p, s);
         case 128:
-            if (kCausal && UsePairKernel() && DmaRowGroups(p, kCausal) == 2) {
-                return LaunchFlashPair<E, 128>(p, s);
-            }
-            return DmaRowGroups(p, kCausal) == 2 ? LaunchFlashDma<E, 128, 2, kCausal>(p, s)
-                                                 : LaunchFlashWide<E, 128, kCausal>(p, s);
+            if (kCausal && UsePairs(p)) return LaunchFlashPair<E, 128>(p, s);
+            return LaunchFlashWide<E, 128, kCausal>(p, s);
         case 160: return LaunchFlash<E, 160, kCausal>(p, s);
         case 192: return LaunchFlash<E, 192, kCausal>(p, s);
         case 256: return LaunchFlash<E, 256, kCausal>(p, s);
@@ -2505,24 +1888,11 @@ int LaunchForDim(const sca_flash_params& p, hipStream_t s) {
 
 bool Aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-// Packed batches run the wide-row kernel. A measurement build reads SCA_FLASH_WIDE_VARLEN=0 to
-// run the 8-wave DMA kernel instead.
-bool UseWideVarlen() {
-#ifdef SCA_MEASUREMENT_BUILD
-    static const bool on = [] {
-        const char* env = std::getenv("SCA_FLASH_WIDE_VARLEN");
-        return env == nullptr || std::atoi(env) != 0;
-    }();
-    return on;
-#else
-    return true;
-#endif
-}
-
-// One launch over a packed batch: the 128-row geometry, one workgroup per (work entry, head).
+// One launch over a packed batch: the wide kernel, one workgroup per (work entry, head).
 template <typename E, int D, bool kCausal>
 int LaunchFlashVarlen(const sca_flash_varlen_params& v, hipStream_t s) {
-    using G = DmaGeom<D, 4, 2>;
+    using G = WideGeom<D>;
+    static_assert(G::BM == 128, "the work list's row tiles are 128 rows");
     // 32-bit buffer offsets: a sequence's rows plus the wide kernel's ring overrun must fit.
     const int64_t rows_k = v.max_seq_kv + 8 * G::BN;
     if (rows_k * v.k_ss * 2 >= (1LL << 31) || rows_k * v.v_ss * 2 >= (1LL << 31)) {
@@ -2552,26 +1922,14 @@ int LaunchFlashVarlen(const sca_flash_varlen_params& v, hipStream_t s) {
     p.scale = v.scale;
     p.causal = v.causal;
     p.dtype = v.dtype;
-    if (UseWideVarlen()) {
-        using W = WideGeom<D>;
-        static_assert(W::BM == G::BM, "the work list's row tiles fit either kernel");
-        if (const int rc = EnsureLdsLimit<&flash_fwd_wide_kernel<E, D, kCausal, true>>(
-                W::LDS_BYTES, "flash LDS limit")) {
-            return rc;
-        }
-        hipLaunchKernelGGL((flash_fwd_wide_kernel<E, D, kCausal, true>),
-                           dim3(static_cast<unsigned>(blocks)), dim3(W::THREADS), W::LDS_BYTES, s,
-                           p, 0, VarlenArgs{v.cu_seqlens_q, v.cu_seqlens_kv, v.tiles});
-        return CheckLaunch("flash_fwd_wide_kernel (varlen)", s);
-    }
-    if (const int rc =
-            EnsureLdsLimit<&flash_fwd_dma_kernel<E, D, 4, 2, kCausal, true>>(G::LDS_BYTES, "flash LDS limit")) {
+    if (const int rc = EnsureLdsLimit<&flash_fwd_wide_kernel<E, D, kCausal, true>>(
+            G::LDS_BYTES, "flash LDS limit")) {
         return rc;
     }
-    hipLaunchKernelGGL((flash_fwd_dma_kernel<E, D, 4, 2, kCausal, true>),
+    hipLaunchKernelGGL((flash_fwd_wide_kernel<E, D, kCausal, true>),
                        dim3(static_cast<unsigned>(blocks)), dim3(G::THREADS), G::LDS_BYTES, s, p,
                        0, VarlenArgs{v.cu_seqlens_q, v.cu_seqlens_kv, v.tiles});
-    return CheckLaunch("flash_fwd_dma_kernel (varlen)", s);
+    return CheckLaunch("flash_fwd_wide_kernel (varlen)", s);
 }
 
 template <typename E>
@@ -2587,9 +1945,9 @@ int LaunchVarlenTyped(const sca_flash_varlen_params& v, hipStream_t s) {
 int LdsBytesFor(int64_t head_dim) {
     switch (head_dim) {
         case 32: return FlashGeom<32>::LDS_BYTES;
-        case 64: return DmaGeom<64, 4, 2>::LDS_BYTES;
+        case 64: return std::max(WideGeom<64>::LDS_BYTES, PairGeom<64>::LDS_BYTES);
         case 96: return FlashGeom<96>::LDS_BYTES;
-        case 128: return DmaGeom<128, 4, 2>::LDS_BYTES;
+        case 128: return std::max(WideGeom<128>::LDS_BYTES, PairGeom<128>::LDS_BYTES);
         case 160: return FlashGeom<160>::LDS_BYTES;
         case 192: return FlashGeom<192>::LDS_BYTES;
         case 256: return FlashGeom<256>::LDS_BYTES;
@@ -2604,14 +1962,6 @@ using sca_hip::SetError;
 
 extern "C" {
 
-#if defined(SCA_MEASUREMENT_BUILD) && defined(SCA_STAMPS)
-// Measurement builds only: copies the wide kernel's region clocks ([blocks*4][9] uint32).
-int sca_hip_debug_wide_stamps(uint32_t* host, int64_t count) {
-    return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(sca_hip::g_wide_stamps),
-                                                static_cast<size_t>(count) * 4));
-}
-#endif
-
 int64_t sca_hip_flash_lds_bytes(int32_t head_dim, int64_t elem_bytes) {
     if (elem_bytes != 2) return -1;
     return sca_hip::LdsBytesFor(head_dim);
@@ -2623,8 +1973,9 @@ int sca_hip_flash_tile(int32_t head_dim, int32_t* block_m, int32_t* block_n, int
         return SetError(SCA_E_UNSUPPORTED_HEAD_DIM,
                         "flash: no tile for head_dim=" + std::to_string(head_dim));
     }
-    // D = 64 / 128 run the DMA-fed kernel; the other head dims the register-staged one.
-    const bool dma = head_dim == 64 || head_dim == 128;
+    // D = 64 / 128 report the wide kernel (every non-causal and every large causal grid); the
+    // other head dims the register-staged one.
+    const bool wide = head_dim == 64 || head_dim == 128;
     int32_t bn = 0, nw = 0, ns = 0;
     switch (head_dim) {
         case 32: bn = sca_hip::FlashGeom<32>::BN; nw = sca_hip::FlashGeom<32>::WAVES;
@@ -2639,10 +1990,10 @@ int sca_hip_flash_tile(int32_t head_dim, int32_t* block_m, int32_t* block_n, int
                   ns = sca_hip::FlashGeom<256>::STAGES; break;
         default: break;
     }
-    if (dma) {
-        bn = sca_hip::DmaGeom<64, 4, 2>::BN;
-        nw = sca_hip::DmaGeom<64, 4, 2>::WAVES;
-        ns = sca_hip::DmaGeom<64, 4, 2>::STAGES;
+    if (wide) {
+        bn = sca_hip::WideGeom<64>::BN;
+        nw = sca_hip::WideGeom<64>::WAVES;
+        ns = sca_hip::WideGeom<64>::SLOTS;
     }
     if (block_m != nullptr) *block_m = sca_hip::kBlockM;
     if (block_n != nullptr) *block_n = bn;

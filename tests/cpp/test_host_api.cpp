@@ -186,9 +186,9 @@ void DispatchRules() {
     const std::string text = dispatcher.Explain(sca::AttentionConfig{}, Shape(1024, 1024));
     CHECK(Has(text, "backend=") && Has(text, "tile={bm=") && Has(text, "workspace=") &&
           Has(text, "reason="));
-    // MI355X tiles: 128 query rows per workgroup; 8 waves up to D=128, 4 above.
+    // MI355X tiles: 128 query rows per workgroup, 4 waves (the wide kernel up to D=128).
     CHECK(dispatcher.Select(sca::AttentionConfig{}, Shape(1024, 1024, 128)).tile.block_m == 128);
-    CHECK(dispatcher.Select(sca::AttentionConfig{}, Shape(1024, 1024, 128)).tile.warps == 8);
+    CHECK(dispatcher.Select(sca::AttentionConfig{}, Shape(1024, 1024, 128)).tile.warps == 4);
     CHECK(dispatcher.Select(sca::AttentionConfig{}, Shape(1024, 1024, 256)).tile.warps == 4);
     CHECK(sca::AttentionDispatcher::ReloadDispatchTable(nullptr).ok());
     CHECK(!sca::AttentionDispatcher::ReloadDispatchTable("table.json").ok());
