@@ -246,9 +246,10 @@ SCA_HIP_API int sca_hip_decode_splitk_paged(const sca_decode_params* params, voi
 /* Allocation-free variant of sca_hip_decode_splitk (contiguous or paged, as page_table says).
  * No counterpart in the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). partial_m/l/o
- * and batch_order must be NULL: the split partials (at most 32 MiB:
+ * and batch_order must be NULL: the split partials (at most 16 MiB:
  * 4*sca_hip_decode_partial_elements(...) bytes) and the ranking scratch live in a static device
- * array, one per GPU, held until the process ends. Larger split counts fail with
+ * array, one per GPU the library is loaded on (reserved for every process that loads it, used
+ * or not), held until the process ends. Larger split counts fail with
  * SCA_E_WORKSPACE. Every call on one GPU shares that array: calls that overlap on one GPU (on
  * different streams) race; calls ordered on one stream are safe. */
 SCA_HIP_API int sca_hip_decode_splitk_noalloc(const sca_decode_params* params, void* stream);

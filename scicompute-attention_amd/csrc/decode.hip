@@ -1051,7 +1051,7 @@ int ValidateDecode(const sca_decode_params* p, bool paged) {
 // ---- allocation-free variant: the split partials and the ranking scratch live in a static
 // device array instead of caller memory ---------------------------------------------------------
 
-constexpr int64_t kNoAllocPartialBytes = int64_t{32} << 20;        // split-K partials
+constexpr int64_t kNoAllocPartialBytes = int64_t{16} << 20;        // split-K partials
 constexpr int64_t kNoAllocOrderBytes = int64_t{2} * kMaxOrderedBatch * 4;  // batch_order
 constexpr int kNoAllocMaxDevices = 64;
 

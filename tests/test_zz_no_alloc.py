@@ -92,7 +92,7 @@ def test_noalloc_rejects_scratch_arguments_and_oversized_partials(hip):
         H.decode_splitk_noalloc(p)  # caller scratch is refused, not silently ignored
     assert e.value.code == 2008
     p, bufs, _ = _paged_params(case, with_scratch=False)
-    p.num_splits = 65535  # 20*32*65535*66*4 B of partials: beyond the 32 MiB maximum
+    p.num_splits = 65535  # 20*32*65535*66*4 B of partials: beyond the 16 MiB maximum
     with pytest.raises(H.HipError) as e:
         H.decode_splitk_noalloc(p)
     assert e.value.code == 2008 and "static scratch" in str(e.value)
