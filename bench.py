@@ -550,9 +550,13 @@ def host_threads():
     return max(n, 1)
 
 
+# PCI device ids that rocm-smi may report in place of a product name.
+PCI_NAMES = {"0x75a3": "AMD Instinct MI355X", "0x75a0": "AMD Instinct MI350X"}
+
+
 def device_name(probe):
-    """The device's marketing name; HIP reports an empty name on some images, then rocm-smi's
-    product name (or the architecture) stands in."""
+    """The device's marketing name: HIP's, else rocm-smi's product name (a PCI device id is
+    translated, or dropped), else None."""
     name = probe.name.decode().strip()
     if name:
         return name
@@ -563,11 +567,13 @@ def device_name(probe):
             for key in ("Card Series", "Card series", "Card Model", "Card model", "Card SKU",
                         "Marketing Name", "Device Name"):
                 val = str(card.get(key, "")).strip()
-                if val and val.upper() != "N/A":
+                if val.lower() in PCI_NAMES:
+                    return PCI_NAMES[val.lower()]
+                if val and val.upper() != "N/A" and not val.lower().startswith("0x"):
                     return val
     except (OSError, ValueError, subprocess.SubprocessError, AttributeError):
         pass
-    return probe.arch_name.decode().split(":")[0]
+    return None
 
 
 def load_traffic(name):
@@ -609,7 +615,7 @@ def main():
     res = {}
     if "prefill" in parts:
         res["c2_causal"] = bench_flash(args.steps, args.warmup, True, prewarm_s=args.prewarm)
-        res["c2_noncausal"] = bench_flash(args.steps, args.warmup, False)
+        res["c2_noncausal"] = bench_flash(args.steps, args.warmup, False, prewarm_s=args.prewarm)
     if "gqa" in parts:
         res["c3_gqa"] = bench_flash_gqa(max(5, args.steps // 5), 3, prewarm_s=args.prewarm)
     if "paged" in parts:
@@ -662,7 +668,9 @@ def main():
             "ms_per_step": round(pg["ms"], 4), "steps": args.paged_steps,
             "splits": pg["splits"], "slot_waves": pg["slot_waves"],
             "workload": "C5 paged decode bf16, 64 seqs L~U[512,16384], bs=16, Hq=32, Hkv=8, "
-                        "D=128, permuted block table, append 1 token/seq per step",
+                        "D=128, permuted block table, append 1 token/seq per step; the K/V "
+                        "pool repeats one seeded 16M-element random chunk (values do not change "
+                        "the work)",
             "roofline": {"bound": "hbm", "achieved": round(pg["gbps"], 1), "peak": PEAK_HBM_GBPS,
                          "unit": "GB/s", "frac": round(pg["gbps"] / PEAK_HBM_GBPS, 4),
                          "traffic": load_traffic("paged_c5")},

@@ -3,11 +3,15 @@
 #include <cstddef>
 #include <cstdint>
 #include <limits>
+#include <string>
+
+#include "core/status.hpp"
 
 namespace sca {
 namespace detail {
 
-// Small integer helpers for host code; overflow is reported, never wrapped.
+// Integer helpers shared by host-side code. Overflow is detected, never ignored.
+
 template <typename T>
 inline constexpr T CeilDiv(T value, T divisor) noexcept {
     return (value + divisor - 1) / divisor;
@@ -15,7 +19,7 @@ inline constexpr T CeilDiv(T value, T divisor) noexcept {
 
 template <typename T>
 inline constexpr bool IsAligned(T value, T alignment) noexcept {
-    return alignment != 0 && value % alignment == 0;
+    return alignment != 0 && (value % alignment) == 0;
 }
 
 template <typename T>
@@ -25,14 +29,15 @@ inline constexpr T AlignUp(T value, T alignment) noexcept {
 
 template <typename T>
 inline constexpr T Min(T a, T b) noexcept {
-    return b < a ? b : a;
+    return a < b ? a : b;
 }
 
 template <typename T>
 inline constexpr T Max(T a, T b) noexcept {
-    return a < b ? b : a;
+    return a > b ? a : b;
 }
 
+// Returns false (and the caller reports an error) when the product does not fit in int64_t.
 inline bool CheckedMul(int64_t a, int64_t b, int64_t* out) noexcept {
     if (a < 0 || b < 0) return false;
     if (a != 0 && b > std::numeric_limits<int64_t>::max() / a) return false;
@@ -48,3 +53,4 @@ inline bool CheckedMulSize(size_t a, size_t b, size_t* out) noexcept {
 
 }  // namespace detail
 }  // namespace sca
+
