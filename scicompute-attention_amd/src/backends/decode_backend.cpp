@@ -26,11 +26,11 @@ int64_t PartialElements(int64_t batch, int64_t heads, int64_t splits, int64_t he
 
 // Explicit split counts are honoured up to the table's cap; otherwise the table decides.
 int64_t ResolveSplits(int64_t requested, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
-                      int64_t seq_kv, int slot_waves = 4) {
+                      int64_t seq_kv, int64_t head_dim, int slot_waves = 4) {
     const auto& th = detail::kDispatchThresholds;
     if (requested > 0) return requested < th.max_splits ? requested : th.max_splits;
     return detail::DecodeSplits(batch, num_heads, num_kv_heads, seq_kv,
-                                DeviceCapability::ForDevice(0).sm_count, slot_waves);
+                                DeviceCapability::ForDevice(0).sm_count, slot_waves, head_dim);
 }
 
 // Points the partial pointers of `p` into the pooled FP32 scratch (m | l | O).
@@ -71,7 +71,7 @@ public:
         CapabilityReport report;
         report.recommended_backend = BackendKind::kDecode;
         const int64_t splits = ResolveSplits(cfg.num_splits, shape.batch, shape.num_heads,
-                                             shape.num_kv_heads, shape.seq_kv);
+                                             shape.num_kv_heads, shape.seq_kv, shape.head_dim);
         report.workspace_bytes = WorkspaceBytes(cfg, shape);
         std::string reason;
         if (!DeviceCapability::GpuAvailable()) {
@@ -98,7 +98,7 @@ public:
 
     size_t WorkspaceBytes(const AttentionConfig& cfg, const AttentionShape& shape) const override {
         const int64_t splits = ResolveSplits(cfg.num_splits, shape.batch, shape.num_heads,
-                                             shape.num_kv_heads, shape.seq_kv);
+                                             shape.num_kv_heads, shape.seq_kv, shape.head_dim);
         if (splits <= 1) return 0;
         return static_cast<size_t>(
                    PartialElements(shape.batch, shape.num_heads, splits, shape.head_dim)) *
@@ -130,7 +130,7 @@ public:
             return fail(AttnStatusCode::kUnsupportedFeature, "decode backend: no GPU device");
         }
         const int64_t splits = ResolveSplits(cfg.num_splits, shape.batch, shape.num_heads,
-                                             shape.num_kv_heads, shape.seq_kv);
+                                             shape.num_kv_heads, shape.seq_kv, shape.head_dim);
 
         AttentionResult result;
         result.out = sci::Tensor(sci::TensorShape({shape.batch, shape.num_heads, shape.seq_q,
@@ -215,9 +215,12 @@ public:
         return report;
     }
 
+    // An estimate from the shape alone (one wave per slot over seq_kv keys); a run under the
+    // cache's length-aware plan binds, and reports in stats.workspace_bytes, what it uses.
     size_t WorkspaceBytes(const AttentionConfig& cfg, const AttentionShape& shape) const override {
         const int64_t splits = ResolveSplits(cfg.num_splits, shape.batch, shape.num_heads,
-                                             shape.num_kv_heads, shape.seq_kv, /*slot_waves=*/1);
+                                             shape.num_kv_heads, shape.seq_kv, shape.head_dim,
+                                             /*slot_waves=*/1);
         if (splits <= 1) return 0;
         return static_cast<size_t>(
                    PartialElements(shape.batch, shape.num_heads, splits, shape.head_dim)) *
@@ -316,11 +319,14 @@ sci::Result<AttentionResult> RunPaged(const sci::Tensor& q, const PagedKVCache& 
     const int64_t seq_kv_bound = kv_cfg.num_blocks * block_size;
     int64_t splits =
         ResolveSplits(cfg.num_splits, num_seqs, num_heads, kv_cfg.num_kv_heads, seq_kv_bound,
-                      /*slot_waves=*/1);
+                      head_dim, /*slot_waves=*/1);
     int32_t slot_waves = 0;
     // With the cache's own page table, its host-side lengths say how ragged the batch is; the
     // MFMA kernel (fp16/bf16, head_dim 64 or 128, power-of-two pages) then takes the split count
-    // and slot work split of the length-aware plan.
+    // and slot work split of the length-aware plan. Lengths the caller passes in
+    // params.seq_lens (device memory) do not feed the plan: the kernel reads them, so results
+    // follow them exactly, while the plan is fitted to the cache's host lengths (which a decode
+    // loop passing its own lengths, with this step's token, tracks to within a token).
     const bool mfma_shape = kv_cfg.dtype != sci::DType::kFloat32 &&
                             (head_dim == 64 || head_dim == 128) &&
                             (block_size & (block_size - 1)) == 0;
@@ -395,7 +401,7 @@ DecodeConfig RecommendDecodeConfig(const AttentionShape& shape, const DeviceCapa
     DecodeConfig cfg;
     cfg.max_splits = detail::kDispatchThresholds.max_splits;
     cfg.num_splits = detail::DecodeSplits(shape.batch, shape.num_heads, shape.num_kv_heads,
-                                          shape.seq_kv, cap.sm_count);
+                                          shape.seq_kv, cap.sm_count, 4, shape.head_dim);
     return cfg;
 }
 

@@ -225,7 +225,8 @@ void sca_recommend_tile(const ScaConfig* cfg, const ScaShape* shape, int32_t* ti
     tile4[3] = t.stages;
 }
 int64_t sca_decode_splits(const ScaShape* s, int64_t cu_count) {
-    return sca::detail::DecodeSplits(s->batch, s->num_heads, s->num_kv_heads, s->seq_kv, cu_count);
+    return sca::detail::DecodeSplits(s->batch, s->num_heads, s->num_kv_heads, s->seq_kv, cu_count,
+                                     4, s->head_dim);
 }
 int sca_paged_decode_plan(const int64_t* lengths, int64_t batch, int64_t num_heads,
                           int64_t num_kv_heads, int64_t cu_count, int64_t* splits,

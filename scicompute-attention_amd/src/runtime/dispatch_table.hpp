@@ -44,16 +44,27 @@ inline constexpr DispatchThresholds kDispatchThresholds{
 //    8 splits, 5.95 against 5.47 at 64; 4 x 16384: 8, 5.84 against 5.66 at 32; 1 x 65536: 32,
 //    5.60 against 5.22 at 64).
 //  - One wave per slot: splits are added until every CU holds `workgroups_per_cu` workgroups.
+//  - head_dim outside {64, 128} (the VALU kernel, a workgroup per (sequence, split, 1-8 heads)):
+//    unsplit once the batch gives every CU a workgroup, else splits until every CU holds four,
+//    with no cap at 8 (fp16, H_q 32, H_kv 8, D 96: 4 x 16384 keys 32 splits, 4.34 TB/s against
+//    3.37 at 8; 16 x 4096 8 splits, 4.63, the best of 1..32; 64 x 4096 unsplit 5.05 against
+//    5.10 at 4). fp32 with D 64 or 128 runs the VALU kernel under the MFMA rule (16 x 4096,
+//    D 128: 5.21 TB/s at 8 splits against 5.52 at 4).
 // Each split keeps at least `min_tokens_per_split` keys.
 inline int64_t DecodeSplits(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
-                            int64_t seq_kv, int64_t cu_count, int slot_waves = 4) {
+                            int64_t seq_kv, int64_t cu_count, int slot_waves = 4,
+                            int64_t head_dim = 128) {
     const auto& th = kDispatchThresholds;
     if (batch < 1 || num_kv_heads < 1 || seq_kv < 1) return 1;
     const int64_t group = num_heads / num_kv_heads;
     const int64_t slots = num_kv_heads * ((group + 15) / 16);
     const int64_t cus = cu_count > 0 ? cu_count : 256;
     int64_t splits;
-    if (slot_waves == 1) {
+    const bool mfma = head_dim == 64 || head_dim == 128;
+    if (!mfma) {
+        const int64_t jobs = batch * slots;
+        splits = jobs >= cus ? 1 : (4 * cus + jobs - 1) / jobs;
+    } else if (slot_waves == 1) {
         const int64_t wgs_per_split = batch * ((slots + 3) / 4);
         splits = (th.workgroups_per_cu * cus + wgs_per_split - 1) / wgs_per_split;
     } else {

@@ -90,3 +90,10 @@ def test_plan_rejects_invalid_heads():
 ])
 def test_contiguous_decode_splits(B, S, want):
     assert H.decode_splits(H.AttentionShape(B, 1, S, 32, 8, 128), CUS) == want
+
+
+@pytest.mark.parametrize("B,S,want", [(4, 16384, 32), (16, 4096, 8), (64, 4096, 1), (1, 1024, 2)])
+def test_contiguous_decode_splits_valu_head_dim(B, S, want):
+    # head_dim 96 runs the VALU kernel: splits until every CU holds four workgroups, no cap at
+    # 8, and at least min_tokens_per_split keys per split (the 1 x 1024 case)
+    assert H.decode_splits(H.AttentionShape(B, 1, S, 32, 8, 96), CUS) == want
