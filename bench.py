@@ -560,6 +560,9 @@ def device_name(probe):
     name = probe.name.decode().strip()
     if name:
         return name
+    if "rocprof" in os.environ.get("LD_PRELOAD", ""):
+        # under the profiler a helper program would start with the GPU already initialised
+        return None
     try:
         out = subprocess.run(["rocm-smi", "--showproductname", "--json"], capture_output=True,
                              text=True, timeout=30).stdout
