@@ -807,8 +807,7 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
         if (kb >= ke) return;
         const int my_q = qt * BM + rg * 32 + lr;
         const int lim = min(seq_kv - 1, my_q + diag);
-        // Keys above lim_j read as -inf (lim_j = -1 masks the whole tile: the score tile past
-        // the range's end is computed from a stale slot and must not move the maximum).
+        // Keys above lim_j read as -inf.
         auto mask = [&](int jt, int lim_j, floatx16& sv) {
             const int kbase = jt * BN + wkey_base + 4 * hh;
 #pragma unroll
@@ -899,11 +898,13 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
         // between the two MFMA runs of the step so that each has VALU and transcendental work
         // to hide: under QK(j+1) the second half of tile j's weights; under PV(j) tile j+1's
         // maximum, exponent arguments and first-half weights (with the current maximum; the
-        // rare move of the maximum redoes them after PV).
-        auto step = [&]<int S, bool MASK>(int j, floatx16& s_in, uint32_t (&ph_in)[4], float sh_in,
-                                          floatx16& s_out, uint32_t (&ph_out)[4], float& sh_out) {
+        // rare move of the maximum redoes them after PV). The range's last step (LAST) has no
+        // next tile: it only finishes tile j's weights and runs PV(j).
+        auto step = [&]<int S, bool MASK, bool LAST = false>(
+                        int j, floatx16& s_in, uint32_t (&ph_in)[4], float sh_in, floatx16& s_out,
+                        uint32_t (&ph_out)[4], float& sh_out) {
             vec8 kf[G::KS];
-            {
+            if constexpr (!LAST) {
                 const uint8_t* base = lds8 + (S ^ 1) * G::TILE_BYTES;
 #pragma unroll
                 for (int ks = 0; ks < G::KS; ++ks) {
@@ -929,18 +930,20 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) pw[i] = ph_in[i];
-            floatx16 acc;
+            if constexpr (!LAST) {
+                floatx16 acc;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+                for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
-            for (int ks = 0; ks < G::KS; ++ks) acc = M::mma(kf[ks], qf[ks], acc);
-            s_out = acc;
+                for (int ks = 0; ks < G::KS; ++ks) acc = M::mma(kf[ks], qf[ks], acc);
+                s_out = acc;
 #pragma unroll
-            for (int i = 0; i < G::KS; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSchedValuTrans, 3, 0);
+                for (int i = 0; i < G::KS; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(kSchedValuTrans, 3, 0);
+                }
+                if constexpr (MASK) mask(j + 1, lim, s_out);
             }
-            if constexpr (MASK) mask(j + 1, j + 1 < ke ? lim : -1, s_out);
             vec8 pb0 = __builtin_bit_cast(vec8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
             vec8 pb1 = __builtin_bit_cast(vec8, make_uint4(pw[4], pw[5], pw[6], pw[7]));
             WaitLdsTied(va, pb0, pb1);
@@ -949,14 +952,16 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
                 o[dt] = M::mma(va[2 * dt], pb0, o[dt]);
                 o[dt] = M::mma(va[2 * dt + 1], pb1, o[dt]);
             }
-            const float lm = prep(s_out, ph_out, sh_out);
+            if constexpr (!LAST) {
+                const float lm = prep(s_out, ph_out, sh_out);
 #pragma unroll
-            for (int i = 0; i < 2 * G::DT; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSchedValuTrans, 6, 0);
+                for (int i = 0; i < 2 * G::DT; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(kSchedValuTrans, 6, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                fix(lm, s_out, ph_out, sh_out);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            fix(lm, s_out, ph_out, sh_out);
             WaitVm<0>();
             gsync();
         };
@@ -964,8 +969,8 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
         uint32_t ph_next[4];
         float sh_next;
         int j = kb;
-        // Steps whose next tile needs no mask, then the rest (the diagonal tile and the range's
-        // end); each run alternates the two register sets and slots by the step's parity.
+        // Steps whose next tile needs no mask, then the rest up to the range's last step; each
+        // run alternates the two register sets and slots by the step's parity.
         auto run = [&]<bool MASK>(int j_end) {
             if (j < j_end && (j & 1)) {
                 step.template operator()<1, MASK>(j, s_cur, ph_cur, sh_cur, s_next, ph_next, sh_next);
@@ -989,7 +994,12 @@ __global__ __launch_bounds__(PairGeom<D>::THREADS, 1) void flash_fwd_pair_kernel
             }
         };
         run.template operator()<false>(min(ke, n_plain) - 1);
-        run.template operator()<true>(ke);
+        run.template operator()<true>(ke - 1);
+        if (j & 1) {
+            step.template operator()<1, true, true>(j, s_cur, ph_cur, sh_cur, s_next, ph_next, sh_next);
+        } else {
+            step.template operator()<0, true, true>(j, s_cur, ph_cur, sh_cur, s_next, ph_next, sh_next);
+        }
     };
     float4* const mquad = reinterpret_cast<float4*>(lds8);
     if (g == 0) {
