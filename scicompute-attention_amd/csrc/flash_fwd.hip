@@ -1577,6 +1577,7 @@ __global__ __launch_bounds__(WideGeom<D>::THREADS, 1) void flash_fwd_wide_kernel
             }
         };
         auto qk = [&](int r, int ks) __attribute__((always_inline)) {
+            if (!next_ok) return;  // the last tile has no S(j+1)
             if (ks == 0) {
                 A::first_v(s_out[r], kf[0], qf[r][0]);
             } else {
